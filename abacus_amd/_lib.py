@@ -1,0 +1,151 @@
+"""ctypes binding of libabacus_moe.so (declarations in include/abacus_moe.h).
+
+The library is the only compute path for device tensors: if it is missing the
+first call raises, there is no fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "libabacus_moe.so"
+
+F32 = 0
+BF16 = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); must match include/abacus_moe.h
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "abacus_moe_last_error": (ctypes.c_char_p, []),
+    "abacus_moe_abi_version": (_I, []),
+    "abacus_moe_hist_len": (_I64, [_I64, _I64]),
+    "abacus_moe_router_ws_bytes": (_I64, [_I64, _I64, _I]),
+    "abacus_moe_router_wgrad_ws_bytes": (_I64, [_I64, _I64, _I64]),
+    "abacus_moe_router_fwd": (
+        _I,
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P, _P, _P, _P],
+    ),
+    "abacus_moe_route_scan": (_I, [_P, _I64, _I64, _I64, _P, _F, _I, _P, _P, _P, _P]),
+    "abacus_moe_permute_gather": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
+    "abacus_moe_gateup_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
+    "abacus_moe_down_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_combine_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_combine_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P]),
+    "abacus_moe_down_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "abacus_moe_down_bwd_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_gateup_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_gateup_bwd_wgrad": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "abacus_moe_unpermute_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_router_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "abacus_router_gating_bwd": (_I, [_P, _P, _P, _I64, _I64, _F, _I, _P, _P]),
+    "abacus_router_update_bias": (_I, [_P, _I64, _I64, _F, _I, _P, _P]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libabacus_moe.so once and declare every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built: run `python -m abacus_amd.build` "
+                    "(the MoE layer has no non-HIP implementation)"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+class KernelTimer:
+    """Records a pair of HIP events around every entry-point call made while active.
+
+    The events go to torch's current stream, which is the stream every entry
+    point is launched on, so (end - start) is that call's device time.
+    """
+
+    def __init__(self) -> None:
+        self.events: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+
+    def __enter__(self) -> "KernelTimer":
+        global _timer
+        _timer = self
+        return self
+
+    def __exit__(self, *exc) -> None:
+        global _timer
+        _timer = None
+
+    def totals_ms(self) -> dict[str, tuple[float, int]]:
+        """name -> (total milliseconds, number of calls); synchronises."""
+        torch.cuda.synchronize()
+        out: dict[str, tuple[float, int]] = {}
+        for name, a, b in self.events:
+            ms, n = out.get(name, (0.0, 0))
+            out[name] = (ms + a.elapsed_time(b), n + 1)
+        return out
+
+
+_timer: KernelTimer | None = None
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point that returns a status code; raise on failure."""
+    lib = load()
+    timer = _timer
+    if timer is not None:
+        start = torch.cuda.Event(enable_timing=True)
+        start.record()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.abacus_moe_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+    if timer is not None:
+        end = torch.cuda.Event(enable_timing=True)
+        end.record()
+        timer.events.append((name, start, end))
+
+
+def query(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return F32
+    if dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"abacus_amd MoE kernels support float32 and bfloat16, got {dtype}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    """Device address of a contiguous tensor (None -> NULL)."""
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("kernel operands must be contiguous")
+    p = t.data_ptr()
+    if p % 16 != 0 and t.numel() > 0:
+        raise ValueError("kernel operands must be 16-byte aligned")
+    return p
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

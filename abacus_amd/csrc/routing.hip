@@ -1,0 +1,870 @@
+// Router, dispatch and combine kernels of the MoE layer (gfx950).
+//
+// Reference semantics (all citations relative to the abacus source tree):
+//   abacus/moe/router.py:45      logits = x @ w_DE; scores = sigmoid(logits)
+//   abacus/moe/router.py:47-48   selection = scores + expert_bias_E; top-k indices (descending)
+//   abacus/moe/router.py:49-51   weights = gather(scores) / sum * route_scale
+//   abacus/moe/router.py:57-70   bias += speed * sign(sum(counts) - E * counts)
+//   abacus/moe/moe.py:72-77      expert-major, ascending-token dispatch order
+//   abacus/moe/moe.py:81-85      out = sum over experts (ascending) of y * weight
+//
+// Every intermediate that the reference rounds to the activation dtype is
+// rounded here too (round_to<T>), so that routing is reproducible bit for bit
+// from the saved logits.
+#include <algorithm>
+
+#include "common.h"
+
+namespace abacus {
+
+constexpr int kRouteTB = 16;   // tokens per router / permute block (one MFMA row tile)
+constexpr int kMaxE = 64;      // experts handled by the fused router
+constexpr int kMaxK = 8;       // slots per token handled by the fused kernels
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// One 16x16 MFMA step over one 16-byte fragment per operand.  For bf16 the
+// fragment is 8 consecutive k of one row/column (v_mfma_f32_16x16x32_bf16).
+// For fp32 the 4 consecutive k of a fragment are fed to 4 successive
+// v_mfma_f32_16x16x4_f32: lane group g supplies k = 4g + j in step j, and
+// both operands follow the same assignment, so the sum over k is complete.
+template <typename T> struct Mma16;
+template <> struct Mma16<uint16_t> {
+  static constexpr int kKB = 32;
+  __device__ static inline void run(f32x4_t& acc, const Vec16& a, const Vec16& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mma16<float> {
+  static constexpr int kKB = 16;
+  __device__ static inline void run(f32x4_t& acc, const Vec16& a, const Vec16& b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bits_f32(a.w[j]), bits_f32(b.w[j]), acc, 0, 0, 0);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// W (D, E) -> Wt (E_pad, D), rows e >= E zero.  Makes every router operand
+// k-contiguous for the MFMA fragments and the dgrad row reads.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void transpose_router_weight_kernel(const T* __restrict__ w, T* __restrict__ wt, int D, int E,
+                                               int E_pad) {
+  int64_t n = (int64_t)E_pad * D;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    int e = (int)(i / D);
+    int d = (int)(i % D);
+    wt[i] = (e < E) ? w[(int64_t)d * E + e] : from_f32<T>(0.0f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K1: fused router.  One block = 16 tokens x all experts; the 4 waves split
+// the D reduction (k-blocks interleaved), partials are summed in LDS in a
+// fixed order, then one thread per token runs the sigmoid / bias / top-k /
+// renormalise epilogue and bumps the block's expert histogram.
+// ---------------------------------------------------------------------------
+template <typename T, int NF>
+__global__ __launch_bounds__(256) void router_fwd_kernel(
+    const T* __restrict__ x, const T* __restrict__ wt, const T* __restrict__ bias, int T_, int D, int E, int K,
+    float route_scale, T* __restrict__ logits, T* __restrict__ weights, int64_t* __restrict__ indices,
+    int32_t* __restrict__ idx32, float* __restrict__ score, int32_t* __restrict__ hist) {
+  constexpr int VEC = VecTraits<T>::kN;
+  constexpr int KB = Mma16<T>::kKB;
+  constexpr int EP = NF * 16;
+  __shared__ float red[4][kRouteTB][EP];
+  __shared__ float s_sc[kRouteTB][EP];
+  __shared__ float s_sel[kRouteTB][EP];
+  __shared__ int s_cnt[kMaxE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int t0 = blockIdx.x * kRouteTB;
+  if (tid < kMaxE) s_cnt[tid] = 0;
+
+  f32x4_t acc[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int row = t0 + (lane & 15);
+  const bool row_ok = row < T_;
+  const T* xrow = x + (int64_t)(row_ok ? row : 0) * D;
+  const int kg = (lane >> 4) * VEC;
+  const bool vec_ok = (D % VEC) == 0;  // rows are 16-byte aligned only then
+  for (int kb = wave * KB; kb < D; kb += 4 * KB) {
+    const int k = kb + kg;
+    Vec16 a, b[NF];
+    if (vec_ok) {
+      const bool k_ok = k < D;
+      a = (row_ok && k_ok) ? ld16(xrow + k) : zero16();
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        b[f] = k_ok ? ld16(wt + (int64_t)(f * 16 + (lane & 15)) * D + k) : zero16();
+    } else {
+      a = zero16();
+#pragma unroll
+      for (int f = 0; f < NF; ++f) b[f] = zero16();
+      for (int i = 0; i < VEC; ++i) {
+        if (k + i < D) {
+          if (row_ok) VecTraits<T>::set(a, i, to_f32<T>(xrow[k + i]));
+#pragma unroll
+          for (int f = 0; f < NF; ++f)
+            VecTraits<T>::set(b[f], i, to_f32<T>(wt[(int64_t)(f * 16 + (lane & 15)) * D + k + i]));
+        }
+      }
+    }
+#pragma unroll
+    for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a, b[f]);
+  }
+  // acc[f][r] = partial logit of token 4*(lane/16)+r, expert f*16 + lane%16
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][f * 16 + (lane & 15)] = acc[f][r];
+  __syncthreads();
+
+  for (int i = tid; i < kRouteTB * EP; i += 256) {
+    const int tok = i / EP, e = i % EP;
+    const float l = ((red[0][tok][e] + red[1][tok][e]) + red[2][tok][e]) + red[3][tok][e];
+    const int t = t0 + tok;
+    if (e < E && t < T_) {
+      const float lr = round_to<T>(l);
+      logits[(int64_t)t * E + e] = from_f32<T>(lr);
+      const float s = round_to<T>(sigmoid_f32_cr(lr));
+      s_sc[tok][e] = s;
+      s_sel[tok][e] = round_to<T>(s + to_f32<T>(bias[e]));
+    }
+  }
+  __syncthreads();
+
+  if (tid < kRouteTB && t0 + tid < T_) {
+    const int tok = tid;
+    const int t = t0 + tok;
+    uint64_t taken = 0;
+    float picked[kMaxK];
+    int picked_e[kMaxK];
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      if (k < K) {
+        int best_e = -1;
+        float best = 0.f;
+        bool best_nan = false;
+        for (int e = 0; e < E; ++e) {
+          if ((taken >> e) & 1ull) continue;
+          const float v = s_sel[tok][e];
+          const bool v_nan = v != v;
+          // torch.topk orders NaN above every number; ties keep the lower index.
+          const bool better = (best_e < 0) || (v_nan && !best_nan) || (!v_nan && !best_nan && v > best);
+          if (better) {
+            best_e = e;
+            best = v;
+            best_nan = v_nan;
+          }
+        }
+        taken |= 1ull << best_e;
+        picked_e[k] = best_e;
+        picked[k] = s_sc[tok][best_e];
+        sum += picked[k];
+        atomicAdd(&s_cnt[best_e], 1);
+      }
+    }
+    const float denom = round_to<T>(sum);
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      if (k < K) {
+        const float w = round_to<T>(round_to<T>(picked[k] / denom) * route_scale);
+        const int64_t o = (int64_t)t * K + k;
+        weights[o] = from_f32<T>(w);
+        indices[o] = picked_e[k];
+        idx32[o] = picked_e[k];
+        score[o] = picked[k];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < E) hist[(int64_t)blockIdx.x * E + tid] = s_cnt[tid];
+}
+
+// ---------------------------------------------------------------------------
+// K2: expert offsets.  hist (nb, E) -> counts, offsets (exclusive scan over
+// experts) and base[b][e] = first dispatched row of block b's tokens for e.
+// Applies the auxiliary-loss-free bias step when requested.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restrict__ hist, int nb, int E,
+                                                          int64_t R, T* __restrict__ bias, float speed,
+                                                          int32_t* __restrict__ base, int32_t* __restrict__ counts,
+                                                          int32_t* __restrict__ offsets) {
+  __shared__ int part[16][kMaxE];
+  __shared__ int cnt[kMaxE];
+  __shared__ int off[kMaxE + 1];
+  const int tid = threadIdx.x;
+  const int e = tid & 63;
+  const int q = tid >> 6;
+  const int per = (nb + 15) / 16;
+  const int b0 = q * per;
+  const int b1 = min(nb, b0 + per);
+  int p = 0;
+  if (e < E)
+    for (int b = b0; b < b1; ++b) p += hist[(int64_t)b * E + e];
+  part[q][e] = p;
+  __syncthreads();
+  if (tid < kMaxE) {
+    int c = 0;
+    for (int i = 0; i < 16; ++i) c += part[i][tid];
+    cnt[tid] = c;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int i = 0; i < E; ++i) {
+      off[i] = run;
+      run += cnt[i];
+    }
+    off[E] = run;
+  }
+  __syncthreads();
+  if (tid < E) {
+    counts[tid] = cnt[tid];
+    offsets[tid] = off[tid];
+    if (bias != nullptr) {
+      // violation = sum(counts) - counts * E  (router.py:68); step = sign(violation)
+      const int64_t violation = R - (int64_t)cnt[tid] * E;
+      const float step = violation > 0 ? 1.0f : (violation < 0 ? -1.0f : 0.0f);
+      const float inc = round_to<T>(speed * step);
+      bias[tid] = from_f32<T>(to_f32<T>(bias[tid]) + inc);
+    }
+  }
+  if (tid == 0) offsets[E] = off[E];
+  if (e < E) {
+    int run = off[e];
+    for (int i = 0; i < q; ++i) run += part[i][e];
+    for (int b = b0; b < b1; ++b) {
+      base[(int64_t)b * E + e] = run;
+      run += hist[(int64_t)b * E + e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K3: permutation + gather.  Wave 0 ranks the block's 16 tokens inside each
+// expert with one ballot per expert (ascending token order), giving every
+// (token, slot) its dispatched row; then the whole block copies each token
+// row once from HBM and writes it to its K destinations.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict__ x, const int32_t* __restrict__ idx,
+                                                             const int32_t* __restrict__ base, int T_, int D, int E,
+                                                             int K, int32_t* __restrict__ pos,
+                                                             int32_t* __restrict__ perm, T* __restrict__ xp) {
+  constexpr int VEC = VecTraits<T>::kN;
+  __shared__ int s_pos[kRouteTB][kMaxK];
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * kRouteTB;
+  if (tid < 64) {
+    const int lane = tid;
+    const int t = t0 + lane;
+    const bool valid = lane < kRouteTB && t < T_;
+    int my_e[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) my_e[k] = (valid && k < K) ? idx[(int64_t)t * K + k] : -1;
+    const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
+    for (int e = 0; e < E; ++e) {
+      int slot = -1;
+#pragma unroll
+      for (int k = 0; k < kMaxK; ++k)
+        if (my_e[k] == e) slot = k;
+      const uint64_t m = __ballot(slot >= 0);
+      if (m == 0) continue;
+      if (slot >= 0) {
+        const int rank = __popcll(m & lt);
+        const int p = base[(int64_t)blockIdx.x * E + e] + rank;
+        pos[(int64_t)t * K + slot] = p;
+        perm[p] = t;
+        s_pos[lane][slot] = p;
+      }
+    }
+  }
+  __syncthreads();
+  const int nvec = D / VEC;
+  const int ntok = min(kRouteTB, T_ - t0);
+  for (int tok = 0; tok < ntok; ++tok) {
+    const T* src = x + (int64_t)(t0 + tok) * D;
+    for (int c = tid; c < nvec; c += 256) {
+      const Vec16 v = ld16(src + c * VEC);
+      for (int k = 0; k < K; ++k) st16(xp + (int64_t)s_pos[tok][k] * D + c * VEC, v);
+    }
+  }
+}
+
+// Sort a token's K slots by expert index so sums run in the reference's
+// ascending-expert order (moe.py:72,85).  Runs on one thread; K <= kMaxK.
+__device__ inline void sort_slots_by_expert(int K, int* e, int* p, float* w) {
+  for (int i = 1; i < K; ++i) {
+    int ke = e[i], kp = p[i];
+    float kw = w[i];
+    int j = i - 1;
+    while (j >= 0 && e[j] > ke) {
+      e[j + 1] = e[j];
+      p[j + 1] = p[j];
+      w[j + 1] = w[j];
+      --j;
+    }
+    e[j + 1] = ke;
+    p[j + 1] = kp;
+    w[j + 1] = kw;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K6: combine.  out[t] = sum_k round(y[pos(t,k)] * w(t,k)), experts ascending,
+// fp32 accumulation, one rounding (the stack().sum(0) of moe.py:85).
+// Gather-reduce per token: no atomics, deterministic.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ y, const T* __restrict__ weights,
+                                                          const int32_t* __restrict__ idx,
+                                                          const int32_t* __restrict__ pos, int T_, int D, int K,
+                                                          T* __restrict__ out) {
+  constexpr int VEC = VecTraits<T>::kN;
+  __shared__ int s_p[kMaxK];
+  __shared__ float s_w[kMaxK];
+  const int tid = threadIdx.x;
+  const int nvec = D / VEC;
+  for (int t = blockIdx.x; t < T_; t += gridDim.x) {
+    if (tid == 0) {
+      int e[kMaxK], p[kMaxK];
+      float w[kMaxK];
+      for (int k = 0; k < K; ++k) {
+        e[k] = idx[(int64_t)t * K + k];
+        p[k] = pos[(int64_t)t * K + k];
+        w[k] = to_f32<T>(weights[(int64_t)t * K + k]);
+      }
+      sort_slots_by_expert(K, e, p, w);
+      for (int k = 0; k < K; ++k) {
+        s_p[k] = p[k];
+        s_w[k] = w[k];
+      }
+    }
+    __syncthreads();
+    for (int c = tid; c < nvec; c += 256) {
+      float acc[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const Vec16 v = ld16(y + (int64_t)s_p[k] * D + c * VEC);
+        const float w = s_w[k];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[i] += round_to<T>(VecTraits<T>::get(v, i) * w);
+      }
+      Vec16 o;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) VecTraits<T>::set(o, i, acc[i]);
+      st16(out + (int64_t)t * D + c * VEC, o);
+    }
+    __syncthreads();
+  }
+}
+
+// Gating backward for one token (router.py:45,49-51), given dL/dweights:
+//   w_k = rho * s_k / S,  S = sum_j s_j
+//   dL/ds_j = (rho * dw_j - sum_k dw_k * w_k) / S
+//   dL/dlogit_j = dL/ds_j * s_j * (1 - s_j)
+__device__ inline void gating_bwd_token(int K, float rho, const float* dw, const float* w, const float* s,
+                                       float denom, float* dl) {
+  float c = 0.f;
+  for (int k = 0; k < K; ++k) c += dw[k] * w[k];
+  for (int k = 0; k < K; ++k) {
+    const float ds = (rho * dw[k] - c) / denom;
+    dl[k] = ds * s[k] * (1.0f - s[k]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// B1: combine backward + gating.  Per token: dy(t,k) = w(t,k) * dout[t]
+// written to the dispatched row, dw(t,k) = <dout[t], y(t,k)>, then the
+// sigmoid / renormalise backward to dL/dlogit for the K selected experts.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ dout, const T* __restrict__ y,
+                                                          const T* __restrict__ weights,
+                                                          const float* __restrict__ score,
+                                                          const int32_t* __restrict__ pos, int T_, int D, int K,
+                                                          float rho, T* __restrict__ dy, float* __restrict__ dlogit) {
+  constexpr int VEC = VecTraits<T>::kN;
+  __shared__ float s_red[4][kMaxK];
+  __shared__ int s_p[kMaxK];
+  __shared__ float s_w[kMaxK];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int nvec = D / VEC;
+  for (int t = blockIdx.x; t < T_; t += gridDim.x) {
+    if (tid < K) {
+      s_p[tid] = pos[(int64_t)t * K + tid];
+      s_w[tid] = to_f32<T>(weights[(int64_t)t * K + tid]);
+    }
+    __syncthreads();
+    float dw[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) dw[k] = 0.f;
+    for (int c = tid; c < nvec; c += 256) {
+      const Vec16 g = ld16(dout + (int64_t)t * D + c * VEC);
+#pragma unroll
+      for (int k = 0; k < kMaxK; ++k) {
+        if (k < K) {
+          const int64_t ro = (int64_t)s_p[k] * D + c * VEC;
+          const Vec16 v = ld16(y + ro);
+          Vec16 o;
+          float part = 0.f;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const float gi = VecTraits<T>::get(g, i);
+            part += gi * VecTraits<T>::get(v, i);
+            VecTraits<T>::set(o, i, gi * s_w[k]);
+          }
+          dw[k] += part;
+          st16(dy + ro, o);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      if (k < K) {
+        const float r = wave_sum(dw[k]);
+        if (lane == 0) s_red[wave][k] = r;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float dwt[kMaxK], w[kMaxK], s[kMaxK], dl[kMaxK];
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) {
+        dwt[k] = ((s_red[0][k] + s_red[1][k]) + s_red[2][k]) + s_red[3][k];
+        w[k] = s_w[k];
+        s[k] = score[(int64_t)t * K + k];
+        sum += s[k];
+      }
+      gating_bwd_token(K, rho, dwt, w, s, round_to<T>(sum), dl);
+      for (int k = 0; k < K; ++k) dlogit[(int64_t)t * K + k] = dl[k];
+    }
+    __syncthreads();
+  }
+}
+
+// Standalone router backward (Router.forward used on its own): dweights -> dlogit.
+template <typename T>
+__global__ void router_gating_bwd_kernel(const T* __restrict__ dweights, const T* __restrict__ weights,
+                                         const float* __restrict__ score, int T_, int K, float rho,
+                                         float* __restrict__ dlogit) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T_) return;
+  float dw[kMaxK], w[kMaxK], s[kMaxK], dl[kMaxK];
+  float sum = 0.f;
+  for (int k = 0; k < K; ++k) {
+    dw[k] = to_f32<T>(dweights[(int64_t)t * K + k]);
+    w[k] = to_f32<T>(weights[(int64_t)t * K + k]);
+    s[k] = score[(int64_t)t * K + k];
+    sum += s[k];
+  }
+  gating_bwd_token(K, rho, dw, w, s, round_to<T>(sum), dl);
+  for (int k = 0; k < K; ++k) dlogit[(int64_t)t * K + k] = dl[k];
+}
+
+// ---------------------------------------------------------------------------
+// B5: un-permute + router dgrad.  dx[t] = sum_k dxp[pos(t,k)]
+//                                        + sum_k dlogit(t,k) * w_DE[:, e(t,k)]
+// Segmented gather-reduce per token (no atomics).  dxp may be null (router
+// used on its own).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void unpermute_bwd_kernel(const T* __restrict__ dxp,
+                                                            const float* __restrict__ dlogit,
+                                                            const int32_t* __restrict__ idx,
+                                                            const int32_t* __restrict__ pos,
+                                                            const T* __restrict__ wt, int T_, int D, int K,
+                                                            T* __restrict__ dx) {
+  constexpr int VEC = VecTraits<T>::kN;
+  __shared__ int s_p[kMaxK];
+  __shared__ int s_e[kMaxK];
+  __shared__ float s_dl[kMaxK];
+  const int tid = threadIdx.x;
+  const int nvec = D / VEC;
+  for (int t = blockIdx.x; t < T_; t += gridDim.x) {
+    if (tid == 0) {
+      int e[kMaxK], p[kMaxK];
+      float dl[kMaxK];
+      for (int k = 0; k < K; ++k) {
+        e[k] = idx[(int64_t)t * K + k];
+        p[k] = dxp ? pos[(int64_t)t * K + k] : 0;
+        dl[k] = dlogit[(int64_t)t * K + k];
+      }
+      sort_slots_by_expert(K, e, p, dl);
+      for (int k = 0; k < K; ++k) {
+        s_e[k] = e[k];
+        s_p[k] = p[k];
+        s_dl[k] = dl[k];
+      }
+    }
+    __syncthreads();
+    if (D % VEC != 0) {
+      // rows not 16-byte aligned: element-wise (small D only)
+      for (int d = tid; d < D; d += 256) {
+        float acc = 0.f;
+        for (int k = 0; k < K; ++k) {
+          if (dxp) acc += to_f32<T>(dxp[(int64_t)s_p[k] * D + d]);
+          acc += s_dl[k] * to_f32<T>(wt[(int64_t)s_e[k] * D + d]);
+        }
+        dx[(int64_t)t * D + d] = from_f32<T>(acc);
+      }
+      __syncthreads();
+      continue;
+    }
+    for (int c = tid; c < nvec; c += 256) {
+      float acc[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+      for (int k = 0; k < K; ++k) {
+        if (dxp) {
+          const Vec16 v = ld16(dxp + (int64_t)s_p[k] * D + c * VEC);
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[i] += VecTraits<T>::get(v, i);
+        }
+        const Vec16 wv = ld16(wt + (int64_t)s_e[k] * D + c * VEC);
+        const float dl = s_dl[k];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[i] += dl * VecTraits<T>::get(wv, i);
+      }
+      Vec16 o;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) VecTraits<T>::set(o, i, acc[i]);
+      st16(dx + (int64_t)t * D + c * VEC, o);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// B6: router weight gradient dW[d, e] = sum_t x[t, d] * dlogit(t, e), with
+// dlogit nonzero only on the K selected experts.  Pass 1: per (d-block,
+// token-chunk) partial sums in LDS columns (one column per thread, no
+// atomics).  Pass 2: fixed-order sum over chunks.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void router_wgrad_partial_kernel(const T* __restrict__ x,
+                                                                   const float* __restrict__ dlogit,
+                                                                   const int32_t* __restrict__ idx, int T_, int D,
+                                                                   int E, int K, int chunk,
+                                                                   float* __restrict__ partial) {
+  __shared__ float acc[kMaxE][256];
+  const int tid = threadIdx.x;
+  const int d = blockIdx.x * 256 + tid;
+  const int c = blockIdx.y;
+  for (int e = 0; e < E; ++e) acc[e][tid] = 0.f;
+  const int ta = c * chunk;
+  const int tb = min(T_, ta + chunk);
+  if (d < D) {
+    for (int t = ta; t < tb; ++t) {
+      const float xv = to_f32<T>(x[(int64_t)t * D + d]);
+      for (int k = 0; k < K; ++k) {
+        const int e = idx[(int64_t)t * K + k];
+        acc[e][tid] += xv * dlogit[(int64_t)t * K + k];
+      }
+    }
+    for (int e = 0; e < E; ++e) partial[((int64_t)c * E + e) * D + d] = acc[e][tid];
+  }
+}
+
+template <typename T>
+__global__ void router_wgrad_reduce_kernel(const float* __restrict__ partial, int nchunks, int D, int E,
+                                           T* __restrict__ dw) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= (int64_t)D * E) return;
+  const int d = (int)(i / E), e = (int)(i % E);
+  float s = 0.f;
+  for (int c = 0; c < nchunks; ++c) s += partial[((int64_t)c * E + e) * D + d];
+  dw[i] = from_f32<T>(s);
+}
+
+// Standalone Router.update_bias(indices) (router.py:57-70).
+template <typename T>
+__global__ __launch_bounds__(1024) void update_bias_kernel(const int64_t* __restrict__ indices, int64_t N, int E,
+                                                           float speed, T* __restrict__ bias) {
+  __shared__ int cnt[kMaxE];
+  const int tid = threadIdx.x;
+  if (tid < kMaxE) cnt[tid] = 0;
+  __syncthreads();
+  for (int64_t i = tid; i < N; i += blockDim.x) {
+    const int64_t e = indices[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid < E) {
+    int64_t total = 0;
+    for (int i = 0; i < E; ++i) total += cnt[i];
+    const int64_t violation = total - (int64_t)cnt[tid] * E;
+    const float step = violation > 0 ? 1.0f : (violation < 0 ? -1.0f : 0.0f);
+    bias[tid] = from_f32<T>(to_f32<T>(bias[tid]) + round_to<T>(speed * step));
+  }
+}
+
+}  // namespace abacus
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+using namespace abacus;
+
+namespace {
+
+inline int elem_size(int dtype) { return dtype == kBF16 ? 2 : 4; }
+inline int vec_elems(int dtype) { return dtype == kBF16 ? 8 : 4; }
+
+int check_dtype(int dtype) {
+  ABACUS_CHECK_ARG(dtype == kF32 || dtype == kBF16, "unsupported dtype code %d (0 = fp32, 1 = bf16)", dtype);
+  return 0;
+}
+
+int check_route_shape(int64_t T, int64_t D, int64_t E, int64_t K, int dtype, bool need_vec = true) {
+  if (check_dtype(dtype)) return 1;
+  ABACUS_CHECK_ARG(T >= 0 && T < (1ll << 31), "token count %lld out of range", (long long)T);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(K >= 1 && K <= E && K <= kMaxK, "top_k %lld: must be in [1, min(n_experts, %d)]",
+                   (long long)K, kMaxK);
+  ABACUS_CHECK_ARG(D >= 1 && D < (1ll << 31), "dim %lld out of range", (long long)D);
+  ABACUS_CHECK_ARG(!need_vec || D % vec_elems(dtype) == 0,
+                   "dim %lld must be a multiple of %d for this dtype", (long long)D, vec_elems(dtype));
+  ABACUS_CHECK_ARG(T * K < (1ll << 31), "routed rows T*K = %lld exceed int32 indexing", (long long)(T * K));
+  return 0;
+}
+
+template <typename T>
+void launch_transpose(const void* w, void* wt, int D, int E, int E_pad, hipStream_t s) {
+  int64_t n = (int64_t)E_pad * D;
+  int blocks = (int)std::min<int64_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(transpose_router_weight_kernel<T>, dim3(blocks), dim3(256), 0, s, (const T*)w, (T*)wt, D, E,
+                     E_pad);
+}
+
+inline int e_pad(int64_t E) { return (int)((E + 15) / 16) * 16; }
+
+}  // namespace
+
+extern "C" {
+
+int64_t abacus_moe_hist_len(int64_t T, int64_t E) { return ((T + kRouteTB - 1) / kRouteTB) * E; }
+
+int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype) {
+  return (int64_t)e_pad(E) * D * elem_size(dtype);
+}
+
+int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
+                          int64_t K, float route_scale, int dtype, void* logits_TE, void* weights_TK,
+                          int64_t* indices_TK, int32_t* idx_TK, float* score_TK, int32_t* hist, void* wt_ws,
+                          void* stream) {
+  if (check_route_shape(T, D, E, K, dtype, false)) return 1;
+  hipStream_t s = (hipStream_t)stream;
+  const int EP = e_pad(E);
+  const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
+  if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+  else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+  ABACUS_CHECK_LAUNCH("router weight transpose");
+  if (nb == 0) return 0;
+#define ROUTER_LAUNCH(TT, NF)                                                                                      \
+  hipLaunchKernelGGL((router_fwd_kernel<TT, NF>), dim3(nb), dim3(256), 0, s, (const TT*)x_TD, (const TT*)wt_ws,    \
+                     (const TT*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale, (TT*)logits_TE,             \
+                     (TT*)weights_TK, indices_TK, idx_TK, score_TK, hist)
+#define ROUTER_DISPATCH_NF(TT)          \
+  switch (EP / 16) {                    \
+    case 1: ROUTER_LAUNCH(TT, 1); break; \
+    case 2: ROUTER_LAUNCH(TT, 2); break; \
+    case 3: ROUTER_LAUNCH(TT, 3); break; \
+    default: ROUTER_LAUNCH(TT, 4); break; \
+  }
+  if (dtype == kBF16) {
+    ROUTER_DISPATCH_NF(uint16_t)
+  } else {
+    ROUTER_DISPATCH_NF(float)
+  }
+#undef ROUTER_DISPATCH_NF
+#undef ROUTER_LAUNCH
+  ABACUS_CHECK_LAUNCH("router_fwd");
+  return 0;
+}
+
+int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, void* bias_E,
+                          float bias_update_speed, int dtype, int32_t* base, int32_t* counts_E,
+                          int32_t* offsets_E1, void* stream) {
+  if (check_dtype(dtype)) return 1;
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(T >= 0 && T * K < (1ll << 31), "bad token count %lld", (long long)T);
+  hipStream_t s = (hipStream_t)stream;
+  const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(route_scan_kernel<uint16_t>, dim3(1), dim3(1024), 0, s, hist, nb, (int)E, T * K,
+                       (uint16_t*)bias_E, bias_update_speed, base, counts_E, offsets_E1);
+  else
+    hipLaunchKernelGGL(route_scan_kernel<float>, dim3(1), dim3(1024), 0, s, hist, nb, (int)E, T * K,
+                       (float*)bias_E, bias_update_speed, base, counts_E, offsets_E1);
+  ABACUS_CHECK_LAUNCH("route_scan");
+  return 0;
+}
+
+int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int32_t* base, int64_t T, int64_t D,
+                              int64_t E, int64_t K, int dtype, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD,
+                              void* stream) {
+  if (check_route_shape(T, D, E, K, dtype)) return 1;
+  const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
+  if (nb == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(permute_gather_kernel<uint16_t>, dim3(nb), dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
+                       base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD);
+  else
+    hipLaunchKernelGGL(permute_gather_kernel<float>, dim3(nb), dim3(256), 0, s, (const float*)x_TD, idx_TK, base,
+                       (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD);
+  ABACUS_CHECK_LAUNCH("permute_gather");
+  return 0;
+}
+
+int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32_t* idx_TK, const int32_t* pos_TK,
+                           int64_t T, int64_t D, int64_t K, int dtype, void* out_TD, void* stream) {
+  if (check_route_shape(T, D, K, K, dtype)) return 1;
+  if (T == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = (int)std::min<int64_t>(T, 1 << 20);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(combine_fwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)y_RD,
+                       (const uint16_t*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (uint16_t*)out_TD);
+  else
+    hipLaunchKernelGGL(combine_fwd_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)y_RD,
+                       (const float*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (float*)out_TD);
+  ABACUS_CHECK_LAUNCH("combine_fwd");
+  return 0;
+}
+
+int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* weights_TK, const float* score_TK,
+                           const int32_t* pos_TK, int64_t T, int64_t D, int64_t K, float route_scale, int dtype,
+                           void* dy_RD, float* dlogit_TK, void* stream) {
+  if (check_route_shape(T, D, K, K, dtype)) return 1;
+  if (T == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = (int)std::min<int64_t>(T, 1 << 20);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(combine_bwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)dout_TD,
+                       (const uint16_t*)y_RD, (const uint16_t*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
+                       route_scale, (uint16_t*)dy_RD, dlogit_TK);
+  else
+    hipLaunchKernelGGL(combine_bwd_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)dout_TD,
+                       (const float*)y_RD, (const float*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
+                       route_scale, (float*)dy_RD, dlogit_TK);
+  ABACUS_CHECK_LAUNCH("combine_bwd");
+  return 0;
+}
+
+int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const float* score_TK, int64_t T,
+                             int64_t K, float route_scale, int dtype, float* dlogit_TK, void* stream) {
+  if (check_dtype(dtype)) return 1;
+  ABACUS_CHECK_ARG(K >= 1 && K <= kMaxK, "top_k %lld: this build supports 1..%d", (long long)K, kMaxK);
+  if (T == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = (int)((T + 255) / 256);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(router_gating_bwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s,
+                       (const uint16_t*)dweights_TK, (const uint16_t*)weights_TK, score_TK, (int)T, (int)K,
+                       route_scale, dlogit_TK);
+  else
+    hipLaunchKernelGGL(router_gating_bwd_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)dweights_TK,
+                       (const float*)weights_TK, score_TK, (int)T, (int)K, route_scale, dlogit_TK);
+  ABACUS_CHECK_LAUNCH("router_gating_bwd");
+  return 0;
+}
+
+int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, const int32_t* idx_TK,
+                             const int32_t* pos_TK, const void* w_DE, void* wt_ws, int64_t T, int64_t D, int64_t E,
+                             int64_t K, int dtype, void* dx_TD, void* stream) {
+  if (check_route_shape(T, D, E, K, dtype, false)) return 1;
+  if (T == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  const int EP = e_pad(E);
+  if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+  else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+  ABACUS_CHECK_LAUNCH("router weight transpose");
+  const int grid = (int)std::min<int64_t>(T, 1 << 20);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(unpermute_bwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)dx_perm_RD,
+                       dlogit_TK, idx_TK, pos_TK, (const uint16_t*)wt_ws, (int)T, (int)D, (int)K,
+                       (uint16_t*)dx_TD);
+  else
+    hipLaunchKernelGGL(unpermute_bwd_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)dx_perm_RD,
+                       dlogit_TK, idx_TK, pos_TK, (const float*)wt_ws, (int)T, (int)D, (int)K, (float*)dx_TD);
+  ABACUS_CHECK_LAUNCH("unpermute_bwd");
+  return 0;
+}
+
+static void router_wgrad_plan(int64_t T, int64_t D, int* chunk, int* nchunks) {
+  const int64_t dblocks = (D + 255) / 256;
+  int64_t want = std::max<int64_t>(1, 512 / dblocks);
+  int64_t nc = std::min<int64_t>(want, std::max<int64_t>(1, (T + 63) / 64));
+  int64_t ch = (T + nc - 1) / nc;
+  if (ch < 1) ch = 1;
+  *chunk = (int)ch;
+  *nchunks = (int)((T + ch - 1) / ch);
+  if (*nchunks < 1) *nchunks = 1;
+}
+
+int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E) {
+  int chunk, nchunks;
+  router_wgrad_plan(T, D, &chunk, &nchunks);
+  return (int64_t)nchunks * E * D * 4;
+}
+
+int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
+                            int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream) {
+  if (check_dtype(dtype)) return 1;
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
+  hipStream_t s = (hipStream_t)stream;
+  int chunk, nchunks;
+  router_wgrad_plan(T, D, &chunk, &nchunks);
+  const dim3 g1((unsigned)((D + 255) / 256), (unsigned)nchunks);
+  const int g2 = (int)((D * E + 255) / 256);
+  // With T == 0 the partial kernel visits no tokens and writes zero partials.
+  if (dtype == kBF16) {
+    hipLaunchKernelGGL(router_wgrad_partial_kernel<uint16_t>, g1, dim3(256), 0, s, (const uint16_t*)x_TD,
+                       dlogit_TK, idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
+  } else {
+    hipLaunchKernelGGL(router_wgrad_partial_kernel<float>, g1, dim3(256), 0, s, (const float*)x_TD, dlogit_TK,
+                       idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
+  }
+  ABACUS_CHECK_LAUNCH("router_wgrad_partial");
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(router_wgrad_reduce_kernel<uint16_t>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks,
+                       (int)D, (int)E, (uint16_t*)dw_DE);
+  else
+    hipLaunchKernelGGL(router_wgrad_reduce_kernel<float>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks, (int)D,
+                       (int)E, (float*)dw_DE);
+  ABACUS_CHECK_LAUNCH("router_wgrad_reduce");
+  return 0;
+}
+
+int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, float speed, int dtype, void* bias_E,
+                              void* stream) {
+  if (check_dtype(dtype)) return 1;
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == kBF16)
+    hipLaunchKernelGGL(update_bias_kernel<uint16_t>, dim3(1), dim3(1024), 0, s, indices, N, (int)E, speed,
+                       (uint16_t*)bias_E);
+  else
+    hipLaunchKernelGGL(update_bias_kernel<float>, dim3(1), dim3(1024), 0, s, indices, N, (int)E, speed,
+                       (float*)bias_E);
+  ABACUS_CHECK_LAUNCH("update_bias");
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,409 @@
+"""MI355X MoE layer: abacus's ``Router``, ``MoE`` and ``MoEExpertParallel`` on HIP kernels.
+
+Same constructors, parameter/buffer names and shapes, initialisation RNG order
+and error messages as the reference modules (abacus/moe/router.py:12-70,
+abacus/moe/moe.py:22-141); the forward and backward run entirely in
+libabacus_moe.so (gfx950), called through ctypes on torch's current stream.
+
+Shape suffixes follow the reference: B batch, L sequence, D model dim,
+M expert hidden dim, E experts, K selected experts, T = B*L tokens,
+R = T*K routed rows.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+import torch.distributed as dist
+
+from abacus_amd import _lib
+from abacus_amd._lib import call, ptr, query
+
+
+def _rank_and_world_size() -> tuple[int, int]:
+    """(rank, world size) of the default process group, (0, 1) without one."""
+    if dist.is_available() and dist.is_initialized():
+        return dist.get_rank(), dist.get_world_size()
+    return 0, 1
+
+
+@dataclasses.dataclass
+class Routing:
+    """Routing decided by the last forward (kept for inspection and tests).
+
+    logits_TE are the exact logits the top-k ran on (dtype of x); counts_E,
+    offsets_E1, perm_R and pos_TK describe the expert-contiguous row order.
+    """
+
+    logits_TE: torch.Tensor
+    weights_TK: torch.Tensor
+    indices_TK: torch.Tensor
+    counts_E: torch.Tensor | None = None
+    offsets_E1: torch.Tensor | None = None
+    perm_R: torch.Tensor | None = None
+    pos_TK: torch.Tensor | None = None
+
+
+def _check_device(x: torch.Tensor, what: str) -> None:
+    if x.device.type != "cuda":
+        raise RuntimeError(
+            f"abacus_amd {what} runs on ROCm (HIP) devices only; got a tensor on {x.device}. "
+            "Move the module and its inputs to a GPU."
+        )
+
+
+def _contig(t: torch.Tensor) -> torch.Tensor:
+    t = t if t.is_contiguous() else t.contiguous()
+    if t.data_ptr() % 16 != 0:
+        t = t.clone()
+    return t
+
+
+def _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale):
+    """Launch the fused router; returns (logits, weights, indices, idx32, score, hist)."""
+    T, D = x_TD.shape
+    E = w_DE.shape[1]
+    dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+    logits = torch.empty(T, E, dtype=x_TD.dtype, device=dev)
+    weights = torch.empty(T, top_k, dtype=x_TD.dtype, device=dev)
+    indices = torch.empty(T, top_k, dtype=torch.int64, device=dev)
+    idx32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
+    score = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    hist = torch.empty(query("abacus_moe_hist_len", T, E), dtype=torch.int32, device=dev)
+    wt = torch.empty(query("abacus_moe_router_ws_bytes", D, E, dt), dtype=torch.uint8, device=dev)
+    call(
+        "abacus_moe_router_fwd", ptr(x_TD), ptr(w_DE), ptr(bias_E), T, D, E, top_k, float(route_scale), dt,
+        ptr(logits), ptr(weights), ptr(indices), ptr(idx32), ptr(score), ptr(hist), ptr(wt), _lib.stream_of(dev),
+    )
+    return logits, weights, indices, idx32, score, hist
+
+
+def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos, dxp):
+    """dx and dW_DE of the router GEMM (plus the un-permute of dxp when given)."""
+    T, D = x_TD.shape
+    E = w_DE.shape[1]
+    K = idx32.shape[1]
+    dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+    s = _lib.stream_of(dev)
+    dx = dw = None
+    if ctx_needs_x:
+        dx = torch.empty_like(x_TD)
+        wt = torch.empty(query("abacus_moe_router_ws_bytes", D, E, dt), dtype=torch.uint8, device=dev)
+        call(
+            "abacus_moe_unpermute_bwd", ptr(dxp), ptr(dlogit), ptr(idx32), ptr(pos), ptr(w_DE), ptr(wt),
+            T, D, E, K, dt, ptr(dx), s,
+        )
+    if ctx_needs_w:
+        dw = torch.empty_like(w_DE)
+        nbytes = query("abacus_moe_router_wgrad_ws_bytes", T, D, E)
+        partial = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+        call("abacus_moe_router_wgrad", ptr(x_TD), ptr(dlogit), ptr(idx32), T, D, E, K, dt, ptr(partial), ptr(dw), s)
+    return dx, dw
+
+
+class _RouterFunction(torch.autograd.Function):
+    """Router.forward (router.py:40-51) as one fused kernel; backward through the gating."""
+
+    @staticmethod
+    def forward(ctx, x_TD, w_DE, bias_E, top_k, route_scale, record):
+        logits, weights, indices, idx32, score, _ = _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale)
+        ctx.save_for_backward(x_TD, w_DE, weights, score, idx32)
+        ctx.route_scale = float(route_scale)
+        ctx.mark_non_differentiable(indices)
+        if record is not None:
+            record["routing"] = Routing(logits, weights, indices)
+        return weights, indices
+
+    @staticmethod
+    def backward(ctx, dweights, _dindices):
+        x_TD, w_DE, weights, score, idx32 = ctx.saved_tensors
+        T, K = weights.shape
+        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+        dlogit = torch.empty(T, K, dtype=torch.float32, device=dev)
+        dweights = _contig(dweights.to(weights.dtype))
+        call(
+            "abacus_router_gating_bwd", ptr(dweights), ptr(weights), ptr(score), T, K, ctx.route_scale, dt,
+            ptr(dlogit), _lib.stream_of(dev),
+        )
+        dx, dw = _router_dgrad_wgrad(
+            ctx.needs_input_grad[0], ctx.needs_input_grad[1], x_TD, w_DE, dlogit, idx32, None, None
+        )
+        return dx, dw, None, None, None, None
+
+
+class _MoEFunction(torch.autograd.Function):
+    """MoE.forward (moe.py:60-86) fused: router -> dispatch -> grouped SwiGLU -> combine."""
+
+    @staticmethod
+    def forward(ctx, x_TD, w_DE, w_gate, w_up, w_down, bias_E, top_k, route_scale, bias_speed, need_grad, record):
+        T, D = x_TD.shape
+        E, _, M = w_gate.shape
+        K = top_k
+        R = T * K
+        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+        s = _lib.stream_of(dev)
+        logits, weights, indices, idx32, score, hist = _router_fwd(x_TD, w_DE, bias_E, K, route_scale)
+        base = torch.empty_like(hist)
+        counts = torch.empty(E, dtype=torch.int32, device=dev)
+        offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        update = bias_speed is not None and bias_speed != 0
+        call(
+            "abacus_moe_route_scan", ptr(hist), T, E, K, ptr(bias_E) if update else None,
+            float(bias_speed) if update else 0.0, dt, ptr(base), ptr(counts), ptr(offsets), s,
+        )
+        pos = torch.empty(T, K, dtype=torch.int32, device=dev)
+        perm = torch.empty(R, dtype=torch.int32, device=dev)
+        xp = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
+        call("abacus_moe_permute_gather", ptr(x_TD), ptr(idx32), ptr(base), T, D, E, K, dt, ptr(pos), ptr(perm), ptr(xp), s)
+        gate = torch.empty(R, M, dtype=x_TD.dtype, device=dev) if need_grad else None
+        up = torch.empty(R, M, dtype=x_TD.dtype, device=dev) if need_grad else None
+        h = torch.empty(R, M, dtype=x_TD.dtype, device=dev)
+        call(
+            "abacus_moe_gateup_fwd", ptr(xp), ptr(w_gate), ptr(w_up), ptr(offsets), R, D, M, E, dt,
+            ptr(gate), ptr(up), ptr(h), s,
+        )
+        y = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
+        call("abacus_moe_down_fwd", ptr(h), ptr(w_down), ptr(offsets), R, M, D, E, dt, ptr(y), s)
+        out = torch.empty(T, D, dtype=x_TD.dtype, device=dev)
+        call("abacus_moe_combine_fwd", ptr(y), ptr(weights), ptr(idx32), ptr(pos), T, D, K, dt, ptr(out), s)
+        if need_grad:
+            ctx.save_for_backward(x_TD, w_DE, w_gate, w_up, w_down, xp, gate, up, h, y, weights, score, idx32, pos, offsets)
+        ctx.route_scale = float(route_scale)
+        if record is not None:
+            record["routing"] = Routing(logits, weights, indices, counts, offsets, perm, pos)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (x_TD, w_DE, w_gate, w_up, w_down, xp, gate, up, h, y, weights, score, idx32, pos,
+         offsets) = ctx.saved_tensors
+        T, D = x_TD.shape
+        E, _, M = w_gate.shape
+        K = idx32.shape[1]
+        R = T * K
+        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+        s = _lib.stream_of(dev)
+        needs = ctx.needs_input_grad
+        dout = _contig(dout.to(x_TD.dtype))
+        dy = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
+        dlogit = torch.empty(T, K, dtype=torch.float32, device=dev)
+        call(
+            "abacus_moe_combine_bwd", ptr(dout), ptr(y), ptr(weights), ptr(score), ptr(pos), T, D, K,
+            ctx.route_scale, dt, ptr(dy), ptr(dlogit), s,
+        )
+        dgate = torch.empty(R, M, dtype=x_TD.dtype, device=dev)
+        dup = torch.empty(R, M, dtype=x_TD.dtype, device=dev)
+        call(
+            "abacus_moe_down_bwd_dgrad", ptr(dy), ptr(w_down), ptr(gate), ptr(up), ptr(offsets), R, M, D, E, dt,
+            ptr(dgate), ptr(dup), s,
+        )
+        dw_down = None
+        if needs[4]:
+            dw_down = torch.empty_like(w_down)
+            call("abacus_moe_down_bwd_wgrad", ptr(h), ptr(dy), ptr(offsets), R, M, D, E, dt, ptr(dw_down), s)
+        dxp = None
+        if needs[0]:
+            dxp = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
+            call(
+                "abacus_moe_gateup_bwd_dgrad", ptr(dgate), ptr(dup), ptr(w_gate), ptr(w_up), ptr(offsets),
+                R, D, M, E, dt, ptr(dxp), s,
+            )
+        dw_gate = dw_up = None
+        if needs[2] or needs[3]:
+            dw_gate = torch.empty_like(w_gate)
+            dw_up = torch.empty_like(w_up)
+            call(
+                "abacus_moe_gateup_bwd_wgrad", ptr(xp), ptr(dgate), ptr(dup), ptr(offsets), R, D, M, E, dt,
+                ptr(dw_gate), ptr(dw_up), s,
+            )
+        dx, dw_DE = _router_dgrad_wgrad(needs[0], needs[1], x_TD, w_DE, dlogit, idx32, pos, dxp)
+        return (dx, dw_DE, dw_gate if needs[2] else None, dw_up if needs[3] else None, dw_down,
+                None, None, None, None, None, None)
+
+
+def _check_operands(x_BLD: torch.Tensor, *params: torch.Tensor) -> None:
+    _check_device(x_BLD, "MoE")
+    for p in params:
+        if p.device != x_BLD.device:
+            raise RuntimeError(f"MoE parameter on {p.device} but input on {x_BLD.device}")
+        if p.dtype != x_BLD.dtype:
+            raise RuntimeError(f"MoE parameter dtype {p.dtype} does not match input dtype {x_BLD.dtype}")
+    _lib.dtype_code(x_BLD.dtype)
+
+
+class Router(torch.nn.Module):
+    """Sigmoid top-k router with DeepSeek-V3 auxiliary-loss-free balancing (router.py:12-70)."""
+
+    def __init__(
+        self,
+        dim: int,
+        n_experts: int,
+        top_k: int,
+        bias_update_speed: float = 1e-3,
+        route_scale: float = 1.0,
+        expert_parallel: bool = False,
+    ):
+        super().__init__()
+        if n_experts < 1:
+            raise ValueError(f"n_experts must be at least 1, got {n_experts}")
+        if not 1 <= top_k <= n_experts:
+            raise ValueError(f"top_k must be in [1, {n_experts}], got {top_k}")
+        self.dim = dim
+        self.n_experts = n_experts
+        self.top_k = top_k
+        self.bias_update_speed = bias_update_speed
+        self.route_scale = route_scale
+        self.expert_parallel = expert_parallel
+        self.w_DE = torch.nn.Parameter(torch.empty(dim, n_experts))  # (D, E)
+        torch.nn.init.xavier_uniform_(self.w_DE)
+        self.register_buffer("expert_bias_E", torch.zeros(n_experts, dtype=self.w_DE.dtype))
+        self.last_routing: Routing | None = None
+
+    def forward(self, x_BLD: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        if self.expert_parallel and _rank_and_world_size()[1] > 1:
+            raise NotImplementedError("expert parallelism across GPUs is not part of the single-GPU abacus_amd build")
+        _check_operands(x_BLD, self.w_DE, self.expert_bias_E)
+        lead = x_BLD.shape[:-1]
+        x_TD = _contig(x_BLD.reshape(-1, self.dim))
+        record: dict = {}
+        if x_TD.shape[0] == 0:
+            weights = x_BLD.new_empty(*lead, self.top_k)
+            indices = torch.empty(*lead, self.top_k, dtype=torch.int64, device=x_BLD.device)
+        else:
+            weights, indices = _RouterFunction.apply(
+                x_TD, self.w_DE, self.expert_bias_E, self.top_k, self.route_scale, record
+            )
+            self.last_routing = record["routing"]
+            weights = weights.reshape(*lead, self.top_k)
+            indices = indices.reshape(*lead, self.top_k)
+        if self.training:
+            self.update_bias(indices)
+        return weights, indices
+
+    @torch.no_grad()
+    def update_bias(self, indices_BLK: torch.Tensor) -> None:
+        """bias += speed * sign(sum(counts) - E * counts) in the bias dtype (router.py:57-70)."""
+        if self.bias_update_speed == 0:
+            return
+        bias = self.expert_bias_E
+        _check_device(bias, "Router.update_bias")
+        idx = _contig(indices_BLK.reshape(-1).to(device=bias.device, dtype=torch.int64))
+        call(
+            "abacus_router_update_bias", ptr(idx), idx.numel(), self.n_experts, float(self.bias_update_speed),
+            _lib.dtype_code(bias.dtype), ptr(bias), _lib.stream_of(bias.device),
+        )
+
+
+def _init_expert_weights(n_experts: int, dim: int, hidden: int):
+    """Per-expert interleaved xavier init: gate[e], up[e], down[e] for e = 0.. (moe.py:48-54)."""
+    gate_EDM = torch.empty(n_experts, dim, hidden)
+    up_EDM = torch.empty(n_experts, dim, hidden)
+    down_EMD = torch.empty(n_experts, hidden, dim)
+    for expert in range(n_experts):
+        torch.nn.init.xavier_uniform_(gate_EDM[expert])
+        torch.nn.init.xavier_uniform_(up_EDM[expert])
+        torch.nn.init.xavier_uniform_(down_EMD[expert])
+    return gate_EDM, up_EDM, down_EMD
+
+
+class MoE(torch.nn.Module):
+    """Top-k mixture of SwiGLU experts (moe.py:22-86) on MI355X kernels."""
+
+    def __init__(
+        self,
+        dim: int,
+        n_experts: int,
+        top_k: int,
+        hidden_dim: int | None = None,
+        bias_update_speed: float = 1e-3,
+        route_scale: float = 1.0,
+    ):
+        super().__init__()
+        self.dim = dim
+        self.n_experts = n_experts
+        self.top_k = top_k
+        self.hidden_dim = dim if hidden_dim is None else hidden_dim
+        if self.hidden_dim < 1:
+            raise ValueError(f"hidden_dim must be at least 1, got {self.hidden_dim}")
+        self.router = Router(
+            dim,
+            n_experts,
+            top_k,
+            bias_update_speed=bias_update_speed,
+            route_scale=route_scale,
+        )
+        gate_EDM, up_EDM, down_EMD = _init_expert_weights(n_experts, dim, self.hidden_dim)
+        self.w_gate_EDM = torch.nn.Parameter(gate_EDM)  # (E, D, M)
+        self.w_up_EDM = torch.nn.Parameter(up_EDM)  # (E, D, M)
+        self.w_down_EMD = torch.nn.Parameter(down_EMD)  # (E, M, D)
+
+    def forward(self, x_BLD: torch.Tensor) -> torch.Tensor:
+        """Routes, dispatches, runs the experts and combines in one autograd node.
+
+        Uses only attributes that MoEExpertParallel also defines, because its
+        single-process forward calls this function unbound (moe.py:140-141).
+        """
+        router = self.router
+        _check_operands(x_BLD, router.w_DE, router.expert_bias_E, self.w_gate_EDM, self.w_up_EDM, self.w_down_EMD)
+        batch_shape = x_BLD.shape[:-1]
+        x_TD = x_BLD.reshape(-1, self.dim)
+        if x_TD.shape[0] == 0:
+            return x_BLD
+        x_TD = _contig(x_TD)
+        record: dict = {}
+        speed = router.bias_update_speed if router.training else None
+        operands = (x_TD, router.w_DE, _contig(self.w_gate_EDM), _contig(self.w_up_EDM), _contig(self.w_down_EMD))
+        need_grad = torch.is_grad_enabled() and any(t.requires_grad for t in operands)
+        out_TD = _MoEFunction.apply(
+            *operands, router.expert_bias_E, self.top_k, router.route_scale, speed, need_grad, record,
+        )
+        router.last_routing = record["routing"]
+        return out_TD.reshape(*batch_shape, self.dim)  # (B, L, D)
+
+
+class MoEExpertParallel(torch.nn.Module):
+    """Top-k SwiGLU experts, one expert per rank (moe.py:89-161).
+
+    With one process it holds every expert and runs MoE.forward; the
+    multi-GPU all-to-all path is not part of this single-GPU build.
+    """
+
+    def __init__(
+        self,
+        dim: int,
+        n_experts: int,
+        top_k: int,
+        hidden_dim: int | None = None,
+        bias_update_speed: float = 1e-3,
+        route_scale: float = 1.0,
+    ):
+        super().__init__()
+        self.dim = dim
+        self.n_experts = n_experts
+        self.top_k = top_k
+        self.hidden_dim = dim if hidden_dim is None else hidden_dim
+        if self.hidden_dim < 1:
+            raise ValueError(f"hidden_dim must be at least 1, got {self.hidden_dim}")
+        self.rank, self.world_size = _rank_and_world_size()
+        if self.world_size > 1 and self.n_experts != self.world_size:
+            raise ValueError(
+                f"expert parallel keeps 1 expert on each rank, "
+                f"got {self.n_experts} experts and world size {self.world_size}"
+            )
+        if self.world_size > 1:
+            raise NotImplementedError("expert parallelism across GPUs is not part of the single-GPU abacus_amd build")
+        self.router = Router(
+            dim,
+            n_experts,
+            top_k,
+            bias_update_speed=bias_update_speed,
+            route_scale=route_scale,
+        )
+        gate_EDM, up_EDM, down_EMD = _init_expert_weights(n_experts, dim, self.hidden_dim)
+        self.w_gate_EDM = torch.nn.Parameter(gate_EDM)  # (E, D, M)
+        self.w_up_EDM = torch.nn.Parameter(up_EDM)  # (E, D, M)
+        self.w_down_EMD = torch.nn.Parameter(down_EMD)  # (E, M, D)
+
+    def forward(self, x_BLD: torch.Tensor) -> torch.Tensor:
+        return MoE.forward(self, x_BLD)

@@ -1,0 +1,228 @@
+"""Benchmark: MoE-layer forward + backward tokens/s on one MI355X.
+
+Workload: the Mixtral-shaped layer (T = 2 x 2048 tokens, d_model 4096, 8 experts,
+top-2 sigmoid router, SwiGLU hidden 14336, bf16 with fp32 accumulation), synthetic
+inputs and N(0, 0.02^2) weights drawn on the GPU.  One step = forward of the layer,
+MSE loss against an N(0, 1) target, backward to x and every parameter (train mode,
+so the router's bias step runs too).
+
+Prints one JSON line with the throughput, the roofline position of the dominant
+kernel (device time from HIP events recorded on the launch stream around every
+entry point during the timed steps), per-kernel figures, and the CPU baseline: the
+oracle's restatement of the reference algorithm timed on the host cores on a bounded
+token sample of the same layer.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+# MI355X published peaks
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+METRIC = "MoE-layer fwd+bwd tokens/sec on 1 MI355X; grouped-GEMM MFMA util %, dispatch GB/s"
+
+GEMM_FLOPS = {  # multiples of R*D*M per entry point
+    "abacus_moe_gateup_fwd": 4,
+    "abacus_moe_down_fwd": 2,
+    "abacus_moe_down_bwd_dgrad": 2,
+    "abacus_moe_down_bwd_wgrad": 2,
+    "abacus_moe_gateup_bwd_dgrad": 4,
+    "abacus_moe_gateup_bwd_wgrad": 4,
+}
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default="mixtral_bf16")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample duration")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def hbm_bytes(wl, name):
+    """Algorithmic HBM bytes per launch for the memory-bound entry points."""
+    s, T, R, D, K = wl.elem_bytes(), wl.tokens, wl.rows, wl.dim, wl.top_k
+    if name == "abacus_moe_permute_gather":
+        return wl.dispatch_bytes()
+    if name == "abacus_moe_combine_fwd":
+        return wl.combine_bytes()
+    if name == "abacus_moe_combine_bwd":
+        # read dout once and every routed y row, write every routed dy row; weights/scores/rows/dlogit
+        return s * D * (T + 2 * R) + (s + 4 + 4 + 4) * R
+    if name == "abacus_moe_unpermute_bwd":
+        return s * D * (R + T) + (4 + 4 + 4) * R
+    return None
+
+
+def cpu_baseline(wl, target_seconds):
+    """Oracle (the reference algorithm restated) on host cores, bounded token sample."""
+    from oracle import moe_oracle as oracle
+    from abacus_amd import workloads as W
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(wl.seed)
+    D, E, M, K = wl.dim, wl.n_experts, wl.hidden, wl.top_k
+    dt = wl.dtype
+    # weights drawn on the GPU (fast) and copied once; same shapes and distribution
+    g = torch.Generator(device="cuda").manual_seed(wl.seed)
+    def draw(*shape):
+        return torch.randn(*shape, device="cuda", generator=g).mul_(0.02).to(dt).cpu()
+    w_DE, wg, wu, wd = draw(D, E), draw(E, D, M), draw(E, D, M), draw(E, M, D)
+    bias = torch.zeros(E, dtype=dt)
+
+    def run(tokens):
+        x = torch.randn(tokens, D, generator=gen).to(dt).requires_grad_()
+        target = torch.randn(tokens, D, generator=gen).to(dt)
+        params = [t.clone().requires_grad_() for t in (w_DE, wg, wu, wd)]
+        t0 = time.perf_counter()
+        out, _ = oracle.moe_forward(x, params[0], bias, params[1], params[2], params[3], K, 1.0)
+        loss = (out.float() - target.float()).pow(2).mean()
+        loss.backward()
+        return time.perf_counter() - t0
+
+    tokens = 16
+    el = run(tokens)  # warm-up + calibration
+    while el < target_seconds / 4 and tokens < wl.tokens:
+        tokens = min(wl.tokens, tokens * 2)
+        el = run(tokens)
+    times = [el]
+    while sum(times) < target_seconds and len(times) < 5:
+        times.append(run(tokens))
+    med = statistics.median(times)
+    cpu_model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": tokens / med,
+        "unit": "tokens/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{wl.name} layer shape (D={D}, E={E}, K={K}, M={M}, {str(dt).replace('torch.', '')}) on "
+                   f"{tokens} of {wl.tokens} tokens, fwd+bwd of the oracle's restatement of router.py:40-70 + "
+                   f"moe.py:60-86, median of {len(times)} runs ({med:.2f} s each); torch CPU threads={cores}, "
+                   f"os.cpu_count={os.cpu_count()}, cpu='{cpu_model}'"),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from abacus_amd import _lib
+    from abacus_amd import workloads as W
+
+    wl = W.ALL[args.workload]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    moe, x, target = W.build_on_device(wl, dev)
+    moe.train()
+    x = x.detach()
+
+    def step():
+        moe.zero_grad(set_to_none=True)
+        xi = x.requires_grad_(wl.backward)
+        out = moe(xi)
+        if wl.backward:
+            loss = (out.float() - target.float()).pow(2).mean()
+            loss.backward()
+        xi.grad = None
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    timer = _lib.KernelTimer()
+    t0 = time.perf_counter()
+    with timer:
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1000.0 * elapsed / args.steps
+    tokens_per_s = wl.tokens / (ms_per_step / 1000.0)
+
+    totals = timer.totals_ms()
+    R, D, M = wl.rows, wl.dim, wl.hidden
+    peak_mfma = PEAK_BF16_TFLOPS if wl.dtype == torch.bfloat16 else PEAK_FP32_TFLOPS
+    kernels = {}
+    for name, (ms, n) in sorted(totals.items(), key=lambda kv: -kv[1][0]):
+        avg_ms = ms / n
+        rec = {"avg_us": round(avg_ms * 1000.0, 2), "calls": n, "share": round(ms / (elapsed * 1000.0), 4)}
+        if name in GEMM_FLOPS:
+            tf = GEMM_FLOPS[name] * R * D * M / (avg_ms / 1000.0) / 1e12
+            rec.update({"tflops": round(tf, 1), "mfma_frac": round(tf / peak_mfma, 4)})
+        b = hbm_bytes(wl, name)
+        if b is not None:
+            gbs = b / (avg_ms / 1000.0) / 1e9
+            rec.update({"gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+        kernels[name] = rec
+
+    gemm_ms = sum(totals[n][0] / totals[n][1] for n in GEMM_FLOPS if n in totals)
+    gemm_tf = wl.gemm_flops() / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
+    dominant = max(totals.items(), key=lambda kv: kv[1][0])[0]
+    d_ms, d_n = totals[dominant]
+    if dominant in GEMM_FLOPS:
+        achieved = GEMM_FLOPS[dominant] * R * D * M / (d_ms / d_n / 1000.0) / 1e12
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak_mfma,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak_mfma, 4), "traffic": None,
+                    "algorithmic_per_launch": GEMM_FLOPS[dominant] * R * D * M}
+    else:
+        b = hbm_bytes(wl, dominant) or 0
+        achieved = b / (d_ms / d_n / 1000.0) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                    "algorithmic_per_launch": b}
+
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if wl.dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (N(0,1) activations and target, N(0,0.02^2) weights, drawn on the GPU)",
+        "config": {"workload": f"{wl.name}: MoE layer fwd+bwd, T={wl.tokens} (batch {wl.batch} x seq {wl.seq}), "
+                               f"D={wl.dim}, E={wl.n_experts}, K={wl.top_k}, M={wl.hidden}",
+                   "tokens": wl.tokens, "d_model": wl.dim, "n_experts": wl.n_experts, "top_k": wl.top_k,
+                   "hidden": wl.hidden},
+        "roofline": roofline,
+        "grouped_gemm": {"tflops": round(gemm_tf, 1), "mfma_frac": round(gemm_tf / peak_mfma, 4),
+                         "ms_per_step": round(gemm_ms, 4)},
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,143 @@
+/*
+ * libabacus_moe — C ABI of the MI355X (gfx950) MoE layer kernels.
+ *
+ * The reference (satyaki-up/abacus) has no native layer: its MoE layer is the
+ * torch-op sequence of abacus/moe/router.py and abacus/moe/moe.py.  Each entry
+ * point below replaces the span of reference ops named in its comment
+ * (file:line relative to the abacus tree); the Python modules in
+ * abacus_amd/moe.py call them in order through ctypes.
+ *
+ * Conventions
+ *   - All pointers are device pointers (HIP, same device), row-major,
+ *     contiguous and 16-byte aligned.  Nothing here allocates, frees or
+ *     synchronises; every launch goes to `stream` (a hipStream_t).
+ *   - dtype: ABACUS_F32 (0) or ABACUS_BF16 (1) for activations and weights;
+ *     index tensors are int32 unless named *_i64; score / dlogit buffers are
+ *     fp32.
+ *   - Return 0 on success, nonzero on a rejected argument (1) or launch
+ *     failure (2); abacus_moe_last_error() gives the message (per thread).
+ *   - Sizes: T tokens, D model dim, E experts (<= 64), K slots per token
+ *     (<= 8), M expert hidden dim, R = T*K routed rows.  D and M must be
+ *     multiples of 8 (bf16) or 4 (fp32).
+ *   - offsets_E1[e] .. offsets_E1[e+1] are the routed rows of expert e in every
+ *     expert-contiguous (R, .) buffer; rows are expert-major and, inside an
+ *     expert, in ascending token order (moe.py:72-77).
+ */
+#ifndef ABACUS_MOE_H
+#define ABACUS_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ABACUS_F32 = 0, ABACUS_BF16 = 1 };
+
+/* ---- library / sizing queries ------------------------------------------ */
+const char* abacus_moe_last_error(void);
+int abacus_moe_abi_version(void);
+/* int32 elements of the per-token-block expert histogram (and of `base`). */
+int64_t abacus_moe_hist_len(int64_t T, int64_t E);
+/* bytes of the transposed router-weight scratch used by router_fwd / unpermute_bwd. */
+int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
+/* bytes of the fp32 partial-sum scratch used by router_wgrad. */
+int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E);
+
+/* ---- forward ------------------------------------------------------------ */
+
+/* Replaces router.py:45-51 (logits GEMM, sigmoid, + expert_bias_E, topk,
+ * gather, renormalise, * route_scale) and the bincount of router.py:65.
+ * Outputs: logits_TE (dtype, the exact logits routing used), weights_TK
+ * (dtype), indices_TK_i64 (descending selection, ties -> lower expert),
+ * idx_TK (int32 copy), score_TK (fp32 value of the dtype-rounded selected
+ * sigmoid scores), hist (abacus_moe_hist_len ints). */
+int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
+                          int64_t K, float route_scale, int dtype, void* logits_TE, void* weights_TK,
+                          int64_t* indices_TK_i64, int32_t* idx_TK, float* score_TK, int32_t* hist, void* wt_ws,
+                          void* stream);
+
+/* Replaces the per-expert counting of moe.py:73-76 and, when bias_E is not
+ * NULL, Router.update_bias (router.py:57-70) in place.  Produces counts_E,
+ * offsets_E1 and base (per token-block first row of each expert). */
+int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, void* bias_E,
+                          float bias_update_speed, int dtype, int32_t* base, int32_t* counts_E,
+                          int32_t* offsets_E1, void* stream);
+
+/* Replaces the boolean-mask gather x_TD[selected_T] of moe.py:77 for all
+ * experts at once: pos_TK[t,k] = routed row of (t,k), perm_R[r] = token of
+ * row r, x_perm_RD[pos] = x_TD[t]. */
+int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int32_t* base, int64_t T, int64_t D,
+                              int64_t E, int64_t K, int dtype, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD,
+                              void* stream);
+
+/* Replaces moe.py:78-79 for every expert: gate = x @ w_gate[e],
+ * up = x @ w_up[e], h = silu(gate) * up.  gate_RM / up_RM may be NULL
+ * (inference: only h is written). */
+int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const void* w_up_EDM,
+                          const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
+                          void* gate_RM, void* up_RM, void* h_RM, void* stream);
+
+/* Replaces moe.py:80: y = h @ w_down[e] for every expert. */
+int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t* offsets_E1, int64_t R, int64_t M,
+                        int64_t D, int64_t E, int dtype, void* y_RD, void* stream);
+
+/* Replaces moe.py:81-85: out[t] = sum over the token's experts (ascending)
+ * of y[pos(t,k)] * weights_TK[t,k]. */
+int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32_t* idx_TK, const int32_t* pos_TK,
+                           int64_t T, int64_t D, int64_t K, int dtype, void* out_TD, void* stream);
+
+/* ---- backward (autograd of the ops above) -------------------------------- */
+
+/* Backward of moe.py:81-85 and router.py:45,49-51: dy_RD[pos] =
+ * w * dout[t]; dL/dweights = <dout[t], y>; then renormalise and sigmoid
+ * backward to dlogit_TK (fp32, one value per selected expert). */
+int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* weights_TK, const float* score_TK,
+                           const int32_t* pos_TK, int64_t T, int64_t D, int64_t K, float route_scale, int dtype,
+                           void* dy_RD, float* dlogit_TK, void* stream);
+
+/* Backward of moe.py:80 (dgrad) fused with the SwiGLU backward of moe.py:78-79:
+ * dh = dy @ w_down[e]^T; dgate = dh*up*silu'(gate); dup = dh*silu(gate). */
+int abacus_moe_down_bwd_dgrad(const void* dy_RD, const void* w_down_EMD, const void* gate_RM, const void* up_RM,
+                              const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E, int dtype,
+                              void* dgate_RM, void* dup_RM, void* stream);
+
+/* Backward of moe.py:80 (wgrad): dw_down[e] = h_e^T dy_e; zero for empty experts. */
+int abacus_moe_down_bwd_wgrad(const void* h_RM, const void* dy_RD, const int32_t* offsets_E1, int64_t R, int64_t M,
+                              int64_t D, int64_t E, int dtype, void* dw_down_EMD, void* stream);
+
+/* Backward of moe.py:78-79 (dgrad): dx_perm = dgate @ w_gate[e]^T + dup @ w_up[e]^T. */
+int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM,
+                                const void* w_up_EDM, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
+                                int64_t E, int dtype, void* dx_perm_RD, void* stream);
+
+/* Backward of moe.py:78-79 (wgrad): dw_gate[e] = x_e^T dgate_e, dw_up[e] = x_e^T dup_e. */
+int abacus_moe_gateup_bwd_wgrad(const void* x_perm_RD, const void* dgate_RM, const void* dup_RM,
+                                const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
+                                void* dw_gate_EDM, void* dw_up_EDM, void* stream);
+
+/* Backward of the gather of moe.py:77 plus the router GEMM of router.py:45
+ * (dgrad): dx[t] = sum_k dx_perm[pos(t,k)] + sum_k dlogit(t,k) w_DE[:, e(t,k)].
+ * dx_perm_RD may be NULL (router used on its own). */
+int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, const int32_t* idx_TK,
+                             const int32_t* pos_TK, const void* w_DE, void* wt_ws, int64_t T, int64_t D, int64_t E,
+                             int64_t K, int dtype, void* dx_TD, void* stream);
+
+/* Backward of the router GEMM of router.py:45 (wgrad): dw_DE = x^T dlogit. */
+int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
+                            int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream);
+
+/* Backward of router.py:49-51 and the sigmoid of :45 when Router.forward is
+ * used on its own: dL/dweights -> dlogit_TK. */
+int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const float* score_TK, int64_t T,
+                             int64_t K, float route_scale, int dtype, float* dlogit_TK, void* stream);
+
+/* Router.update_bias (router.py:57-70) for an explicit int64 index tensor. */
+int abacus_router_update_bias(const int64_t* indices_i64, int64_t N, int64_t E, float speed, int dtype,
+                              void* bias_E, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ABACUS_MOE_H */

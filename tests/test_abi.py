@@ -1,0 +1,68 @@
+"""The C ABI: libabacus_moe.so loads, exports every symbol include/abacus_moe.h declares,
+the ctypes table matches the header, and argument validation fails cleanly (no GPU needed:
+rejected calls return before any HIP call)."""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+from abacus_amd import _lib
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "abacus_moe.h"
+
+
+def _declarations():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r"^\s*([A-Za-z_][\w\s\*]*?)\b(abacus_\w+)\s*\(([^;]*?)\)\s*;", text, flags=re.M | re.S):
+        args = m.group(3).strip()
+        n = 0 if args in ("", "void") else len(args.split(","))
+        decls[m.group(2)] = n
+    return decls
+
+
+def test_header_declares_entry_points():
+    decls = _declarations()
+    assert len(decls) >= 20
+    assert "abacus_moe_router_fwd" in decls and "abacus_moe_gateup_fwd" in decls
+
+
+def test_ctypes_table_matches_header():
+    decls = _declarations()
+    assert set(decls) == set(_lib.SIGNATURES)
+    for name, nargs in decls.items():
+        assert len(_lib.SIGNATURES[name][1]) == nargs, name
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _declarations():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_queries():
+    lib = _lib.load()
+    assert lib.abacus_moe_abi_version() == 1
+    assert _lib.query("abacus_moe_hist_len", 4096, 8) == (4096 // 16) * 8
+    assert _lib.query("abacus_moe_hist_len", 17, 8) == 2 * 8
+    assert _lib.query("abacus_moe_router_ws_bytes", 4096, 8, _lib.BF16) == 16 * 4096 * 2
+    assert _lib.query("abacus_moe_router_ws_bytes", 1024, 17, _lib.F32) == 32 * 1024 * 4
+    assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8) > 0
+
+
+@pytest.mark.parametrize(
+    "name,args,msg",
+    [
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 65, 2, 1.0, 1) + (None,) * 8, "n_experts"),
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 9, 1.0, 1) + (None,) * 8, "top_k"),
+        ("abacus_moe_permute_gather", (None, None, None, 16, 12, 8, 2, 1, None, None, None, None), "dim"),
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 2, 1.0, 7) + (None,) * 8, "dtype"),
+        ("abacus_moe_gateup_fwd", (None, None, None, None, 16, 64, 30, 8, 0, None, None, None, None), "hidden_dim"),
+        ("abacus_moe_down_fwd", (None, None, None, 16, 64, 64, 0, 0, None, None), "n_experts"),
+    ],
+)
+def test_rejected_arguments_raise_with_message(name, args, msg):
+    with pytest.raises(RuntimeError, match=msg):
+        _lib.call(name, *args)

@@ -1,0 +1,215 @@
+"""MoE layer forward + backward on the GPU against the oracle (CPU, same dtype) at sizes it
+finishes in seconds, and against a torch fp32 evaluation of the same algorithm on the GPU at
+the full workload sizes.  Tolerances (stated per the layer's contract): fp32 rtol 1e-5,
+bf16 rtol 2e-2, each with atol = rtol * rms(reference) so near-zero entries are judged on
+the tensor's scale.  Routing is taken from the kernel (identical-logits contract) so that
+both sides run the same experts."""
+
+import pytest
+import torch
+
+from abacus_amd import _lib
+from abacus_amd import workloads as W
+from abacus.mlp import MLP
+from abacus.moe.moe import MoE, MoEExpertParallel
+from oracle import moe_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+PARAMS = ("router.w_DE", "w_gate_EDM", "w_up_EDM", "w_down_EMD")
+
+
+def rtol_for(dtype):
+    return 1e-5 if dtype == torch.float32 else 2e-2
+
+
+def assert_close_scaled(got, want, rtol, what):
+    got, want = got.float().cpu(), want.float().cpu()
+    rms = float(want.pow(2).mean().sqrt()) if want.numel() else 0.0
+    torch.testing.assert_close(got, want, rtol=rtol, atol=rtol * max(rms, 1e-30), msg=lambda m: f"{what}: {m}")
+
+
+def product_step(moe, x, target, backward=True):
+    """One forward (+ MSE backward) through the HIP path; returns out, x.grad, param grads, routing."""
+    x = x.detach().clone().requires_grad_(backward)
+    moe.zero_grad(set_to_none=True)
+    out = moe(x)
+    grads = {}
+    if backward:
+        loss = (out.float() - target.float()).pow(2).mean()
+        loss.backward()
+        grads = {n: p.grad for n, p in moe.named_parameters()}
+    torch.cuda.synchronize()
+    return out.detach(), (x.grad if backward else None), grads, moe.router.last_routing
+
+
+def reference_step(moe, x, target, indices, compute_dtype, device, backward=True):
+    """The oracle (reference algorithm) with the given routing, in compute_dtype on device."""
+    p = {n: t.detach().to(device=device, dtype=compute_dtype).clone().requires_grad_(backward)
+         for n, t in moe.named_parameters()}
+    bias = moe.router.expert_bias_E.detach().to(device=device, dtype=compute_dtype)
+    xr = x.detach().to(device=device, dtype=compute_dtype).clone().requires_grad_(backward)
+    x_TD = xr.reshape(-1, moe.dim)
+    out, _ = oracle.moe_forward(x_TD, p["router.w_DE"], bias, p["w_gate_EDM"], p["w_up_EDM"], p["w_down_EMD"],
+                                moe.top_k, moe.router.route_scale, indices_TK=indices.to(device))
+    out = out.reshape(x.shape)
+    grads = {}
+    if backward:
+        loss = (out.float() - target.to(device).float()).pow(2).mean()
+        loss.backward()
+        grads = {n: t.grad for n, t in p.items()}
+    return out.detach(), (xr.grad if backward else None), grads
+
+
+def check_against(moe, x, target, compute_dtype, device, rtol, backward=True):
+    moe.eval()  # no bias drift between the two evaluations
+    out, dx, grads, routing = product_step(moe, x, target, backward)
+    idx = routing.indices_TK.reshape(-1, moe.top_k)
+    r_out, r_dx, r_grads = reference_step(moe, x, target, idx, compute_dtype, device, backward)
+    assert_close_scaled(out, r_out, rtol, "out")
+    if backward:
+        assert_close_scaled(dx, r_dx, rtol, "dx")
+        for n in PARAMS:
+            assert_close_scaled(grads[n], r_grads[n], rtol, f"d{n}")
+
+
+# ---------------- oracle on the CPU, same dtype ----------------
+ORACLE_CASES = [
+    (W.TINY_F32, True),
+    (W.MID_F32.with_tokens(1, 1024), True),
+    (W.SKEW_BF16_T64, False),
+]
+
+
+@pytest.mark.parametrize("wl,backward", ORACLE_CASES, ids=[c[0].name for c in ORACLE_CASES])
+def test_matches_cpu_oracle(wl, backward):
+    print(f"\n[moe-oracle] {wl.name} dtype={wl.dtype} bwd={backward}", flush=True)
+    small = wl.dim * wl.hidden * wl.n_experts < 50_000_000
+    moe, x, target = W.build(wl, device=DEV) if small else W.build_on_device(wl, DEV)
+    check_against(moe, x, target, wl.dtype, torch.device("cpu"), rtol_for(wl.dtype), backward)
+
+
+# ---------------- torch fp32 on the GPU, full sizes ----------------
+FULL_CASES = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K]
+
+
+@pytest.mark.parametrize("wl", FULL_CASES, ids=[w.name for w in FULL_CASES])
+def test_matches_fp32_reference_full_size(wl):
+    print(f"\n[moe-full] {wl.name} T={wl.tokens} D={wl.dim} E={wl.n_experts} K={wl.top_k} M={wl.hidden} "
+          f"bwd={wl.backward}", flush=True)
+    moe, x, target = W.build_on_device(wl, DEV)
+    check_against(moe, x, target, torch.float32, DEV, rtol_for(wl.dtype), wl.backward)
+
+
+# ---------------- edge cases (the reference's own test scenarios) ----------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_one_expert_matches_mlp(dtype):
+    """tests/test_moe.py:42-53 on the GPU (E = 1, K = 1 is the dense SwiGLU)."""
+    torch.manual_seed(0)
+    moe = MoE(4 if dtype == torch.float32 else 8, n_experts=1, top_k=1, hidden_dim=8)
+    mlp = MLP(moe.dim, 8)
+    with torch.no_grad():
+        mlp.w_gate_DM.copy_(moe.w_gate_EDM[0])
+        mlp.w_up_DM.copy_(moe.w_up_EDM[0])
+        mlp.w_down_MD.copy_(moe.w_down_EMD[0])
+    moe, mlp = moe.to(DEV, dtype), mlp.to(DEV, dtype)
+    x = torch.randn(2, 3, moe.dim, device=DEV, dtype=dtype)
+    rtol = rtol_for(dtype)
+    assert_close_scaled(moe(x), mlp(x), rtol, "out")
+
+
+def test_forced_routing_leaves_experts_empty():
+    """w_DE = -8 except column 0 = +8, speed 0 (tests/test_moe_ep.py:94-102): experts 1..3 empty."""
+    torch.manual_seed(2)
+    moe = MoE(dim=4, n_experts=4, top_k=1, hidden_dim=8, bias_update_speed=0.0)
+    with torch.no_grad():
+        moe.router.w_DE.fill_(-8)
+        moe.router.w_DE[:, 0] = 8
+    moe = moe.to(DEV)
+    x = torch.randn(2, 3, 4, device=DEV)
+    target = torch.randn(2, 3, 4, device=DEV)
+    moe.train()
+    out, dx, grads, routing = product_step(moe, x, target)
+    assert routing.counts_E.tolist() == [6, 0, 0, 0]
+    for n in ("w_gate_EDM", "w_up_EDM", "w_down_EMD"):
+        assert torch.count_nonzero(grads[n][1:]) == 0
+    r_out, r_dx, r_grads = reference_step(moe, x, target, routing.indices_TK.reshape(-1, 1), torch.float32,
+                                          torch.device("cpu"))
+    assert_close_scaled(out, r_out, 1e-5, "out")
+    assert_close_scaled(dx, r_dx, 1e-5, "dx")
+    for n in PARAMS:
+        assert_close_scaled(grads[n], r_grads[n], 1e-5, n)
+
+
+@pytest.mark.parametrize("T,E,K,rs", [(1, 4, 1, 1.0), (6, 4, 2, 1.5), (37, 8, 3, 1.0), (100, 16, 8, 0.7)])
+def test_small_ragged_shapes(T, E, K, rs):
+    """Token counts off the 16-token block, K up to 8, single-token batches (three empty experts)."""
+    print(f"\n[moe-small] T={T} E={E} K={K} rs={rs}", flush=True)
+    torch.manual_seed(T + E)
+    moe = MoE(dim=16, n_experts=E, top_k=K, hidden_dim=24, route_scale=rs).to(DEV)
+    x = torch.randn(1, T, 16, device=DEV)
+    target = torch.randn(1, T, 16, device=DEV)
+    check_against(moe, x, target, torch.float32, torch.device("cpu"), 1e-5)
+
+
+def test_two_training_steps_track_bias_updates():
+    """Two train-mode iterations (tests/test_moe_ep.py:49-71): outputs, grads and the bias."""
+    torch.manual_seed(1)
+    moe = MoE(dim=16, n_experts=4, top_k=2, hidden_dim=32, bias_update_speed=0.25, route_scale=1.5).to(DEV)
+    moe.train()
+    bias = moe.router.expert_bias_E.detach().cpu().clone()
+    for step in range(2):
+        x = torch.randn(2, 9, 16, device=DEV)
+        target = torch.randn(2, 9, 16, device=DEV)
+        out, dx, grads, routing = product_step(moe, x, target)
+        logits = routing.logits_TE.cpu()
+        _, idx_o, _ = oracle.route(logits, bias, 2, 1.5)
+        assert torch.equal(routing.indices_TK.cpu(), idx_o), step
+        bias = oracle.bias_step(bias, idx_o, 4, 0.25)
+        assert torch.equal(moe.router.expert_bias_E.cpu(), bias), step
+        # the oracle reproduces the output with the same routing
+        r_out, r_dx, _ = reference_step(moe, x, target, idx_o, torch.float32, torch.device("cpu"))
+        assert_close_scaled(out, r_out, 1e-5, "out")
+        assert_close_scaled(dx, r_dx, 1e-5, "dx")
+
+
+def test_one_process_expert_parallel_matches_moe():
+    """tests/test_moe_ep.py:14-23 on the GPU: MoEExpertParallel at world size 1 == MoE."""
+    torch.manual_seed(0)
+    ref = MoE(dim=4, n_experts=4, top_k=2, hidden_dim=8, bias_update_speed=0.1).to(DEV)
+    torch.manual_seed(0)
+    par = MoEExpertParallel(dim=4, n_experts=4, top_k=2, hidden_dim=8, bias_update_speed=0.1).to(DEV)
+    ref.train()
+    par.train()
+    x = torch.randn(2, 3, 4, device=DEV)
+    torch.testing.assert_close(par(x), ref(x))
+    torch.testing.assert_close(par.router.expert_bias_E, ref.router.expert_bias_E)
+
+
+@pytest.mark.parametrize("wl", [W.TINY_F32, W.SKEW_BF16_T512.with_tokens(1, 1000)], ids=["tiny_f32", "skew_bf16_T1000"])
+def test_deterministic(wl):
+    """No atomics on the data path: two runs are bitwise identical."""
+    moe, x, target = W.build_on_device(dataclasses_replace_backward(wl), DEV)
+    moe.eval()
+    a = product_step(moe, x, target)
+    b = product_step(moe, x, target)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    for n in PARAMS:
+        assert torch.equal(a[2][n], b[2][n]), n
+
+
+def dataclasses_replace_backward(wl):
+    import dataclasses
+    return dataclasses.replace(wl, backward=True)
+
+
+def test_empty_batch_returns_input():
+    moe = MoE(8, 4, 2).to(DEV)
+    x = torch.randn(2, 0, 8, device=DEV)
+    assert moe(x) is x
+
+
+def test_native_library_is_what_ran():
+    moe = MoE(8, 4, 2).to(DEV)
+    moe(torch.randn(1, 5, 8, device=DEV))
+    assert _lib._lib is not None and str(_lib.LIB_PATH).endswith("libabacus_moe.so")

@@ -1,0 +1,137 @@
+"""Routing parity on the GPU: indices, weights, per-expert counts, offsets, the permutation
+and the bias step are bit-exact against the oracle given the kernel's own logits
+(router.py:40-70, moe.py:72-77); against torch.sigmoid + torch.topk they agree on every
+token whose selection boundary is not a near-tie."""
+
+import numpy as np
+import pytest
+import torch
+
+from abacus_amd import workloads as W
+from abacus.moe.router import Router
+from oracle import moe_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+# (workload, build on CPU with the exact recipe?)  Large weights are drawn on the GPU.
+CASES = [
+    (W.TINY_F32, True),
+    (W.MID_F32, True),
+    (W.MIXTRAL_BF16, False),
+    (W.SKEW_BF16_T64, False),
+    (W.SKEW_BF16_T512, False),
+    (W.SKEW_BF16_T16K, False),
+]
+
+
+def build(wl, on_cpu):
+    if on_cpu:
+        return W.build(wl, device=DEV)
+    return W.build_on_device(wl, DEV)
+
+
+def _near_tie_tokens(sel, k):
+    """Tokens whose k-th and (k+1)-th selection values are within 4 ulp (torch.sigmoid may be 2 ulp off)."""
+    if k >= sel.shape[-1]:
+        return torch.zeros(sel.shape[0], dtype=torch.bool)
+    v = torch.sort(sel.float(), dim=-1, descending=True).values
+    a, b = v[:, k - 1], v[:, k]
+    ulp = (torch.nextafter(a.to(sel.dtype), torch.tensor(float("inf"), dtype=sel.dtype)).float() - a).abs()
+    return (a - b) <= 4 * ulp
+
+
+@pytest.mark.parametrize("wl,on_cpu", CASES, ids=[c[0].name for c in CASES])
+def test_routing_bit_exact(wl, on_cpu):
+    print(f"\n[routing] {wl.name} T={wl.tokens} D={wl.dim} E={wl.n_experts} K={wl.top_k}", flush=True)
+    moe, x, _ = build(wl, on_cpu)
+    moe.train()
+    bias0 = moe.router.expert_bias_E.detach().clone()
+    with torch.no_grad():
+        moe(x)
+    torch.cuda.synchronize()
+    r = moe.router.last_routing
+    E, K = wl.n_experts, wl.top_k
+    logits = r.logits_TE.cpu()
+    w_o, idx_o, _ = oracle.route(logits, bias0.cpu(), K, moe.router.route_scale)
+    idx_k = r.indices_TK.cpu()
+    assert torch.equal(idx_k, idx_o)
+    assert torch.equal(r.weights_TK.cpu(), w_o)
+    counts, offsets, perm, pos = oracle.dispatch(idx_o, E)
+    assert np.array_equal(r.counts_E.cpu().numpy(), counts)
+    assert np.array_equal(r.offsets_E1.cpu().numpy(), offsets)
+    assert np.array_equal(r.perm_R.cpu().numpy(), perm)
+    assert np.array_equal(r.pos_TK.cpu().numpy(), pos)
+    bias_o = oracle.bias_step(bias0.cpu(), idx_o, E, moe.router.bias_update_speed)
+    assert torch.equal(moe.router.expert_bias_E.cpu(), bias_o)
+
+    # The logits themselves are a GEMM: close to an fp32 product of the same inputs.
+    ref = x.float().reshape(-1, wl.dim) @ moe.router.w_DE.float()
+    tol = 1e-5 if wl.dtype == torch.float32 else 1e-2
+    torch.testing.assert_close(r.logits_TE.float(), ref, rtol=tol, atol=tol * float(ref.std()))
+
+    # Against the literal reference ops: exact top-k sets away from near-ties.
+    sel = torch.sigmoid(logits) + bias0.cpu()
+    torch_idx = torch.topk(sel, K, dim=-1).indices
+    tie = _near_tie_tokens(sel, K)
+    same = (torch.sort(idx_k, -1).values == torch.sort(torch_idx, -1).values).all(-1)
+    print(f"[routing] {wl.name}: near-tie tokens {int(tie.sum())}/{len(tie)}; "
+          f"set mismatches off near-ties {int((~same & ~tie).sum())}", flush=True)
+    assert bool(same[~tie].all())
+
+
+def test_router_known_answer():
+    """The reference's router test (tests/test_moe.py:9-39) through the kernel, dim = 1."""
+    router = Router(dim=1, n_experts=4, top_k=2, bias_update_speed=10.0, route_scale=2.5).to(DEV)
+    with torch.no_grad():
+        router.w_DE.copy_(torch.tensor([[2.0, 0.0, -2.0, 1.0]]))
+        router.expert_bias_E.copy_(torch.tensor([0.0, 0.0, 10.0, 0.0]))
+    x = torch.ones(1, 4, 1, device=DEV)
+    scores = torch.sigmoid(x @ router.w_DE)
+    router.train()
+    weights, indices = router(x)
+    start = torch.tensor([0.0, 0.0, 10.0, 0.0], device=DEV)
+    expected = torch.topk(scores + start, k=2, dim=-1).indices
+    picked = scores.gather(dim=-1, index=expected)
+    torch.testing.assert_close(indices, expected)
+    torch.testing.assert_close(weights, picked / picked.sum(dim=-1, keepdim=True) * 2.5)
+    assert torch.all(indices[..., 0] == 2)
+    assert router.expert_bias_E.tolist() == [-10.0, 10.0, 0.0, 10.0]
+    weights2, indices2 = router(x)
+    stepped = torch.tensor([-10.0, 10.0, 0.0, 10.0], device=DEV)
+    expected2 = torch.topk(scores + stepped, k=2, dim=-1).indices
+    picked2 = scores.gather(dim=-1, index=expected2)
+    torch.testing.assert_close(indices2, expected2)
+    torch.testing.assert_close(weights2, picked2 / picked2.sum(dim=-1, keepdim=True) * 2.5)
+    assert torch.all(indices2[..., 0] == 3) and torch.all(indices2[..., 1] == 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_router_backward_matches_oracle(dtype):
+    """Standalone Router: gradients of sum(weights * g) w.r.t. x and w_DE."""
+    torch.manual_seed(11)
+    T, D, E, K = 50, 64, 8, 3
+    router = Router(D, E, K, route_scale=1.5).to(device=DEV, dtype=dtype)
+    x = torch.randn(T, D, device=DEV, dtype=dtype, requires_grad=True)
+    g = torch.randn(T, K, device=DEV, dtype=dtype)
+    router.eval()
+    w, idx = router(x)
+    (w.float() * g.float()).sum().backward()
+    x_ref = x.detach().cpu().double().requires_grad_()
+    wde_ref = router.w_DE.detach().cpu().double().requires_grad_()
+    logits = x_ref @ wde_ref
+    s = torch.sigmoid(logits)
+    picked = s.gather(-1, idx.cpu())
+    w_ref = picked / picked.sum(-1, keepdim=True) * 1.5
+    (w_ref * g.cpu().double()).sum().backward()
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    for got, want in ((x.grad, x_ref.grad), (router.w_DE.grad, wde_ref.grad)):
+        want = want.float()
+        torch.testing.assert_close(got.float().cpu(), want, rtol=tol, atol=tol * float(want.pow(2).mean().sqrt()))
+
+
+def test_update_bias_explicit_indices():
+    router = Router(4, 4, 2, bias_update_speed=0.5).to(DEV)
+    idx = torch.tensor([[0, 1], [0, 2], [0, 1]], device=DEV)
+    router.update_bias(idx)
+    assert router.expert_bias_E.tolist() == [-0.5, -0.5, 0.5, 0.5]
