@@ -71,21 +71,52 @@ struct GemmArgs {
   int Kdim;                  // reduction length (per half for DUAL_K); unused for WGRAD
 };
 
-template <typename T> struct Mma;
-template <> struct Mma<uint16_t> {
-  static constexpr int kKB = 32;  // k covered by one fragment (4 lane groups x 8)
-  __device__ static inline void run(f32x4_t& acc, const Vec16& a, const Vec16& b) {
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// MFMA policies.  A fragment is 16 bytes per lane: lane l supplies row
+// (l % kRows) and the VEC consecutive k at (l / kRows) * VEC of a k-block of
+// kKB.  For fp32 the 4 values of a fragment feed 4 successive MFMAs (lane
+// group g supplies k = 4g + j in step j; A and B agree, so the sum over k is
+// complete).  Output: lane l holds column (l % kRows) and, in register q,
+// row out_row(l, q).
+template <typename T, int SHAPE> struct MfmaOp;
+template <> struct MfmaOp<uint16_t, 16> {
+  static constexpr int kRows = 16, kKB = 32, kAcc = 4;
+  using Acc = f32x4_t;
+  __device__ static inline void run(Acc& acc, const Vec16& a, const Vec16& b) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                   __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
   }
+  __device__ static inline int out_row(int lane, int q) { return 4 * (lane >> 4) + q; }
 };
-template <> struct Mma<float> {
-  static constexpr int kKB = 16;  // 4 lane groups x 4 k, fed to 4 MFMAs (k = 4g + j)
-  __device__ static inline void run(f32x4_t& acc, const Vec16& a, const Vec16& b) {
+template <> struct MfmaOp<float, 16> {
+  static constexpr int kRows = 16, kKB = 16, kAcc = 4;
+  using Acc = f32x4_t;
+  __device__ static inline void run(Acc& acc, const Vec16& a, const Vec16& b) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bits_f32(a.w[j]), bits_f32(b.w[j]), acc, 0, 0, 0);
   }
+  __device__ static inline int out_row(int lane, int q) { return 4 * (lane >> 4) + q; }
+};
+template <> struct MfmaOp<uint16_t, 32> {
+  static constexpr int kRows = 32, kKB = 16, kAcc = 16;
+  using Acc = f32x16_t;
+  __device__ static inline void run(Acc& acc, const Vec16& a, const Vec16& b) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                  __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+  }
+  __device__ static inline int out_row(int lane, int q) { return 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3); }
+};
+template <> struct MfmaOp<float, 32> {
+  static constexpr int kRows = 32, kKB = 8, kAcc = 16;
+  using Acc = f32x16_t;
+  __device__ static inline void run(Acc& acc, const Vec16& a, const Vec16& b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(bits_f32(a.w[j]), bits_f32(b.w[j]), acc, 0, 0, 0);
+  }
+  __device__ static inline int out_row(int lane, int q) { return 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3); }
 };
 
 // In-register transpose of a VEC x VEC micro-block: in[r] holds VEC
@@ -113,27 +144,19 @@ template <> struct Transpose<float> {
   }
 };
 
-template <typename T, int BM, int BN, int BK, int WM, int WN>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int SHAPE>
 struct Tile {
+  using Op = MfmaOp<T, SHAPE>;
   static constexpr int NT = WM * WN * 64;
   static constexpr int VEC = VecTraits<T>::kN;
   static constexpr int PAD = VEC;                 // 16 bytes of padding per LDS row
   static constexpr int LDK = BK + PAD;
   static constexpr int WTM = BM / WM, WTN = BN / WN;
-  static constexpr int FM = WTM / 16, FN = WTN / 16;
-  static constexpr int KB = Mma<T>::kKB;
+  static constexpr int FR = Op::kRows;
+  static constexpr int FM = WTM / FR, FN = WTN / FR;
+  static constexpr int KB = Op::kKB;
   static_assert(BK % KB == 0, "BK must hold whole MFMA k-blocks");
-  static_assert(WTM % 16 == 0 && WTN % 16 == 0, "wave tile must be whole 16x16 fragments");
-  // k-contiguous operand: one 16B vector per item
-  template <int ROWS> struct KC {
-    static constexpr int ITEMS = ROWS * BK / VEC;
-    static constexpr int PER = (ITEMS + NT - 1) / NT;
-  };
-  // mn-contiguous operand: VEC x VEC micro-blocks
-  template <int ROWS> struct MC {
-    static constexpr int ITEMS = (ROWS / VEC) * (BK / VEC);
-    static constexpr int PER = (ITEMS + NT - 1) / NT;
-  };
+  static_assert(WTM % FR == 0 && WTN % FR == 0, "wave tile must be whole MFMA fragments");
 };
 
 // Load one operand tile (ROWS rows of the LDS [row][k] layout) from global into
@@ -168,8 +191,8 @@ struct OperandLoader {
         }
       } else {
         if (item < ITEMS && tid_rel >= 0) {
-          const int mb = item % (ROWS / VEC);
-          const int kb = item / (ROWS / VEC);
+          const int kb = item % (BK / VEC);
+          const int mb = item / (BK / VEC);
           int gr = row0 + mb * VEC;
           // whole VEC-wide row groups are valid or clamped together (dims % VEC == 0)
           gr = gr < row_lim ? gr : row_lim - VEC;
@@ -193,8 +216,10 @@ struct OperandLoader {
           const int kv = item % (BK / VEC);
           st16(lds + row * ldk + kv * VEC, r[p]);
         } else {
-          const int mb = item % (ROWS / VEC);
-          const int kb = item / (ROWS / VEC);
+          // k-block fastest across lanes: 8 consecutive lanes write one LDS row's
+          // BK contiguous elements, so the 16-byte stores hit distinct banks.
+          const int kb = item % (BK / VEC);
+          const int mb = item / (BK / VEC);
           Vec16 t[VEC];
           Transpose<T>::run(&r[p * VEC], t);
 #pragma unroll
@@ -205,16 +230,23 @@ struct OperandLoader {
   }
 };
 
-template <typename T, int KIND, int BM, int BN, int BK, int WM, int WN>
-__global__ __launch_bounds__(WM* WN * 64) void grouped_gemm_kernel(GemmArgs g) {
+template <typename T, int KIND, int BM, int BN, int BK, int WM, int WN, int SHAPE, int MINB>
+__global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_gemm_kernel(GemmArgs g) {
   using KT = KindTraits<KIND>;
-  using TL = Tile<T, BM, BN, BK, WM, WN>;
-  constexpr int NT = TL::NT, VEC = TL::VEC, LDK = TL::LDK, FM = TL::FM, FN = TL::FN, KB = TL::KB;
+  using TL = Tile<T, BM, BN, BK, WM, WN, SHAPE>;
+  using Op = typename TL::Op;
+  using Acc = typename Op::Acc;
+  constexpr int NT = TL::NT, VEC = TL::VEC, LDK = TL::LDK, FM = TL::FM, FN = TL::FN, KB = TL::KB, FR = TL::FR;
   constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
   constexpr int ROWS_B = KT::DUAL_B ? BN / 2 : BN; // rows of each B operand in LDS
+  static_assert(!KT::DUAL_B || FN % 2 == 0, "dual-B tiles pair gate/up fragments");
 
-  __shared__ __attribute__((aligned(16))) T lds_a[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) T lds_b[2][BN * LDK];
+  constexpr int LDC = BN + VEC;  // row stride of the epilogue's C tile
+  constexpr int kOperandElems = 2 * (BM + BN) * LDK;
+  constexpr int kLdsElems = kOperandElems > BM * LDC ? kOperandElems : BM * LDC;
+  __shared__ __attribute__((aligned(16))) T lds_buf[kLdsElems];
+  T (*lds_a)[BM * LDK] = reinterpret_cast<T (*)[BM * LDK]>(lds_buf);
+  T (*lds_b)[BN * LDK] = reinterpret_cast<T (*)[BN * LDK]>(lds_buf + 2 * BM * LDK);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -265,8 +297,8 @@ __global__ __launch_bounds__(WM* WN * 64) void grouped_gemm_kernel(GemmArgs g) {
   LA la;
   LB lb0;
   LB lb1;
-  // Thread offsets: when both operands are mn-contiguous, give them disjoint
-  // thread ranges so the micro-block loads spread over the whole block.
+  // Thread offsets: when both operands are mn-contiguous and small, give them
+  // disjoint thread ranges so the micro-block loads spread over the block.
   constexpr bool kSplit = KT::A_MC && KT::B_NC && LA::ITEMS <= NT / 2 &&
                           (KT::DUAL_B ? 2 * LB::ITEMS : LB::ITEMS) <= NT / 2;
   const int ta = tid;
@@ -297,20 +329,23 @@ __global__ __launch_bounds__(WM* WN * 64) void grouped_gemm_kernel(GemmArgs g) {
     if (KT::DUAL_B) lb1.store(lds_b[buf] + ROWS_B * LDK, LDK, tb1);
   };
 
-  f32x4_t acc[FM][FN];
+  Acc acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < Op::kAcc; ++q) acc[i][j][q] = 0.f;
 
-  // LDS row of B fragment j for this wave
+  // LDS row of B fragment j for this wave (dual-B: first half gate, second up,
+  // paired so fragment j and j + FN/2 cover the same output columns)
   auto b_frag_row = [&](int j) -> int {
     if (KT::DUAL_B) {
       constexpr int HF = FN / 2;
       const int half = j / HF;
-      return half * (BN / 2) + wn * (TL::WTN / 2) + (j % HF) * 16;
+      return half * (BN / 2) + wn * (TL::WTN / 2) + (j % HF) * FR;
     }
-    return wn * TL::WTN + j * 16;
+    return wn * TL::WTN + j * FR;
   };
 
   if (ktiles > 0) {
@@ -326,122 +361,393 @@ __global__ __launch_bounds__(WM* WN * 64) void grouped_gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int kb = 0; kb < BK / KB; ++kb) {
       Vec16 af[FM], bfr[FN];
-      const int kofs = kb * KB + (lane >> 4) * VEC;
+      const int kofs = kb * KB + (lane / FR) * VEC;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const Vec16*>(As + (wm * TL::WTM + i * 16 + (lane & 15)) * LDK + kofs);
+        af[i] = *reinterpret_cast<const Vec16*>(As + (wm * TL::WTM + i * FR + (lane % FR)) * LDK + kofs);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bfr[j] = *reinterpret_cast<const Vec16*>(Bs + (b_frag_row(j) + (lane & 15)) * LDK + kofs);
+        bfr[j] = *reinterpret_cast<const Vec16*>(Bs + (b_frag_row(j) + (lane % FR)) * LDK + kofs);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) Mma<T>::run(acc[i][j], af[i], bfr[j]);
+        for (int j = 0; j < FN; ++j) Op::run(acc[i][j], af[i], bfr[j]);
     }
     if (kt + 1 < ktiles) store_stage(buf ^ 1);
     __syncthreads();
   }
 
   // ---------------- epilogue ----------------
-  // acc[i][j][r] = C[wm*WTM + i*16 + 4*(lane/16) + r][col(j) + lane%16]
-  const int lr = 4 * (lane >> 4);
-  const int lc = lane & 15;
-  if (KIND == kGateUpFwd) {
-    constexpr int HF = FN / 2;
-    T* G = (T*)g.c0;
-    T* U = (T*)g.c1;
-    T* H = (T*)g.c2;
+  // Phase 1: every wave writes its accumulators, rounded to T (the reference
+  // rounds each product to the activation dtype), into an LDS tile laid out
+  // like the B operand rows: [BM][BN] (dual-B: gate columns, then up columns).
+  // acc[i][j][q] = C[wm*WTM + i*FR + out_row(lane, q)][b_frag_row(j) + lane % FR]
+  T* ctile = lds_buf;  // the operand buffers are free after the last barrier
+  {
+    const int lc = lane % FR;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < HF; ++j) {
-        const int col = n0 + wn * (TL::WTN / 2) + j * 16 + lc;
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row0 + wm * TL::WTM + i * 16 + lr + r;
-          if (row < row_end && col < g.Ndim) {
-            const float gv = round_to<T>(acc[i][j][r]);
-            const float uv = round_to<T>(acc[i][j + HF][r]);
-            const float sg = round_to<T>(silu_f32(gv));
-            const int64_t o = (int64_t)row * g.ldc + col;
-            if (G) G[o] = from_f32<T>(gv);
-            if (U) U[o] = from_f32<T>(uv);
-            H[o] = from_f32<T>(sg * uv);
-          }
-        }
+        for (int q = 0; q < Op::kAcc; ++q)
+          ctile[(wm * TL::WTM + i * FR + Op::out_row(lane, q)) * LDC + b_frag_row(j) + lc] =
+              from_f32<T>(acc[i][j][q]);
+  }
+  __syncthreads();
+
+  // Phase 2: the block walks the output tile in 16-byte vectors (coalesced
+  // global stores) and applies the kind's elementwise epilogue.
+  constexpr int CV = BNH / VEC;  // vectors per output row
+  const int rlim = KT::WGRAD ? g.Mdim : row_end;
+  for (int v = tid; v < BM * CV; v += NT) {
+    const int r = v / CV;
+    const int c = (v % CV) * VEC;
+    const int row = row0 + r;
+    const int col = n0 + c;
+    if (row >= rlim || col >= g.Ndim) continue;
+    const int64_t o = (int64_t)row * g.ldc + col;
+    const Vec16 c0 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + c);
+    if (KIND == kGateUpFwd) {
+      const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
+      Vec16 h;
+#pragma unroll
+      for (int t = 0; t < VEC; ++t) {
+        const float gv = VecTraits<T>::get(c0, t);
+        const float uv = VecTraits<T>::get(c1, t);
+        VecTraits<T>::set(h, t, round_to<T>(silu_f32(gv)) * uv);
       }
-  } else if (KIND == kDownDgrad) {
-    const T* Gi = (const T*)g.x0;
-    const T* Ui = (const T*)g.x1;
-    T* dG = (T*)g.c0;
-    T* dU = (T*)g.c1;
+      if (g.c0) st16((T*)g.c0 + o, c0);
+      if (g.c1) st16((T*)g.c1 + o, c1);
+      st16((T*)g.c2 + o, h);
+    } else if (KIND == kDownDgrad) {
+      const Vec16 gi = ld16((const T*)g.x0 + o);
+      const Vec16 ui = ld16((const T*)g.x1 + o);
+      Vec16 dg, du;
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int col = n0 + wn * TL::WTN + j * 16 + lc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row0 + wm * TL::WTM + i * 16 + lr + r;
-          if (row < row_end && col < g.Ndim) {
-            const int64_t o = (int64_t)row * g.ldc + col;
-            const float dh = round_to<T>(acc[i][j][r]);
-            const float gv = to_f32<T>(Gi[o]);
-            const float uv = to_f32<T>(Ui[o]);
-            const float sig = sigmoid_f32(gv);
-            const float act = round_to<T>(silu_f32(gv));                // silu(g) exactly as forward
-            const float dact = round_to<T>(dh * uv);                    // d(silu(g))
-            const float dg = dact * sig * (1.0f + gv * (1.0f - sig));   // silu'(g)
-            dU[o] = from_f32<T>(dh * act);
-            dG[o] = from_f32<T>(dg);
-          }
-        }
+      for (int t = 0; t < VEC; ++t) {
+        const float dh = VecTraits<T>::get(c0, t);
+        const float gv = VecTraits<T>::get(gi, t);
+        const float uv = VecTraits<T>::get(ui, t);
+        const float sig = sigmoid_f32(gv);
+        const float act = round_to<T>(silu_f32(gv));   // silu(g) exactly as forward
+        const float dact = round_to<T>(dh * uv);       // d(silu(g))
+        VecTraits<T>::set(dg, t, dact * sig * (1.0f + gv * (1.0f - sig)));
+        VecTraits<T>::set(du, t, dh * act);
       }
-  } else if (KIND == kGateUpWgrad) {
-    constexpr int HF = FN / 2;
-    T* C0 = (T*)g.c0 + (int64_t)e * g.c_estride;
-    T* C1 = (T*)g.c1 + (int64_t)e * g.c_estride;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < HF; ++j) {
-        const int col = n0 + wn * (TL::WTN / 2) + j * 16 + lc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row0 + wm * TL::WTM + i * 16 + lr + r;
-          if (row < g.Mdim && col < g.Ndim) {
-            const int64_t o = (int64_t)row * g.ldc + col;
-            C0[o] = from_f32<T>(acc[i][j][r]);
-            C1[o] = from_f32<T>(acc[i][j + HF][r]);
-          }
-        }
-      }
-  } else {
-    T* C = (T*)g.c0 + (KT::WGRAD ? (int64_t)e * g.c_estride : 0);
-    const int rlim = KT::WGRAD ? g.Mdim : row_end;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int col = n0 + wn * TL::WTN + j * 16 + lc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = row0 + wm * TL::WTM + i * 16 + lr + r;
-          if (row < rlim && col < g.Ndim) C[(int64_t)row * g.ldc + col] = from_f32<T>(acc[i][j][r]);
-        }
-      }
+      st16((T*)g.c0 + o, dg);
+      st16((T*)g.c1 + o, du);
+    } else if (KIND == kGateUpWgrad) {
+      const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
+      const int64_t oe = (int64_t)e * g.c_estride + o;
+      st16((T*)g.c0 + oe, c0);
+      st16((T*)g.c1 + oe, c1);
+    } else {
+      st16((T*)g.c0 + (KT::WGRAD ? (int64_t)e * g.c_estride : 0) + o, c0);
+    }
   }
 }
 
-// Tile configuration per (dtype, kind).  The first configuration is shared by
-// every kind: 128 x 128 block tiles, 4 waves of 64 x 64, BK = 64 bf16 / 32 fp32.
-template <typename T> struct Cfg;
-template <> struct Cfg<uint16_t> { static constexpr int BM = 128, BN = 128, BK = 64, WM = 2, WN = 2; };
-template <> struct Cfg<float> { static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2; };
+// ===========================================================================
+// bf16 pipelined kernel (gfx950): 256 x 256 x 32 block tiles, 4 waves of
+// 128 x 128 (v_mfma_f32_32x32x16_bf16), four LDS stages filled by direct
+// global->LDS DMA (global_load_lds_dwordx4: no VGPR staging), three tiles in
+// flight.  Operands keep their memory orientation in LDS:
+//   k-contiguous  ("kc"): [row][32 k]  (4 x 16-byte chunks per row)
+//   mn-contiguous ("mc"): [k][256 mn]  (32 x 16-byte chunks per k row)
+// with the 16-byte chunk index XOR-swizzled per row so that DMA writes,
+// ds_read_b128 (kc fragments) and ds_read_b64_tr_b16 (mc fragments, the LDS
+// transpose read) are free of bank conflicts.  A transposed read gives each
+// lane 4 consecutive k of one column; two of them form the 8-k MFMA operand.
+// ===========================================================================
+namespace pipe {
+
+constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4, NT = 256;
+constexpr int TILE_BYTES = 256 * BK * 2;          // one operand tile: 16 KB
+constexpr int STAGE_BYTES = 2 * TILE_BYTES;       // A + B
+constexpr int LDC = BN + 8;                        // epilogue C tile row stride (bf16)
+constexpr int LDS_BYTES = STAGES * STAGE_BYTES > BM * LDC * 2 ? STAGES * STAGE_BYTES : BM * LDC * 2;
+constexpr int LOADS_PER_TILE = 8;                  // DMA instructions per thread per k-tile (A 4 + B 4)
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16 zero bytes: the DMA source for k beyond a ragged segment's end.
+__device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
+
+__device__ inline int kc_off(int row, int chunk) { return (row * 4 + (chunk ^ ((row >> 2) & 3))) * 16; }
+__device__ inline int mc_off(int k, int chunk) { return (k * 32 + (chunk ^ ((k & 3) << 2))) * 16; }
+
+// global_load_lds_dwordx4 issued through inline asm: the compiler does not
+// model it, so it neither inserts vmcnt(0) before LDS reads of other stages
+// nor before barriers; completion is tracked explicitly with wait_vmcnt<N>().
+// M0 holds the (wave-uniform) LDS destination; lane l's 16 bytes land at
+// M0 + 16 l.
+__device__ inline void dma16(const void* src, char* lds_dst) {
+  const uint32_t lds_addr =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_dst);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+}
+
+// Wait until at most N DMA instructions of this thread are outstanding
+// (vmcnt), without waiting on LDS or export counters.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+// One operand tile -> LDS.  Chunk p of the tile (p = 0..1023) is written by
+// instruction i = p / 256 of wave (p / 64) % 4, lane p % 64.
+//   kc: p -> (row = p / 4, chunk = swizzle^-1): element (row0 + row, k0 + 8 c)
+//   mc: p -> (k = p / 32, chunk):              element (k0 + k, mn0 + 8 c)
+// base1 != null splits the mn range in two halves of 128 (dual-B gate | up).
+template <bool MC>
+__device__ inline void dma_tile(char* tile, const uint16_t* base0, const uint16_t* base1, int64_t ld, int r0,
+                                int r_lim, int k0, int k_lim, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int blk = i * 4 + wave;
+    const int p = blk * 64 + lane;
+    const void* src;
+    if (!MC) {
+      const int row = p >> 2;
+      const int c = (p & 3) ^ ((row >> 2) & 3);
+      int gr = r0 + row;
+      gr = gr < r_lim ? gr : r_lim - 1;
+      const int kk = k0 + c * 8;
+      src = kk < k_lim ? (const void*)(base0 + (int64_t)gr * ld + kk) : (const void*)g_zero16;
+    } else {
+      const int k = p >> 5;
+      const int c = (p & 31) ^ ((k & 3) << 2);
+      int mn = c * 8;
+      const uint16_t* b = base0;
+      if (base1 != nullptr && mn >= 128) {
+        b = base1;
+        mn -= 128;
+      }
+      int gm = r0 + mn;
+      gm = gm < r_lim ? gm : r_lim - 8;
+      const int kk = k0 + k;
+      src = kk < k_lim ? (const void*)(b + (int64_t)kk * ld + gm) : (const void*)g_zero16;
+    }
+    dma16(src, tile + blk * 1024);
+  }
+}
+
+// 32 x 16 MFMA operand fragment (rows or columns f0 .. f0+31, k-step t of 2).
+__device__ inline Vec16 frag_kc(const char* tile, int f0, int t, int lane) {
+  const int r = f0 + (lane & 31);
+  return *reinterpret_cast<const Vec16*>(tile + kc_off(r, 2 * t + (lane >> 5)));
+}
+__device__ inline Vec16 frag_mc(const char* tile, int f0, int t, int lane) {
+  const int grp = lane >> 4, s = lane & 15;
+  const int mn = f0 + 16 * (grp & 1) + 4 * (s & 3);
+  const int k = 16 * t + 8 * (grp >> 1) + (s >> 2);
+  const int b = (mn & 7) * 2;
+  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(tile + mc_off(k, mn >> 3) + b));
+  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(tile + mc_off(k + 4, mn >> 3) + b));
+  Vec16 v;
+  v.w[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+  v.w[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+  v.w[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+  v.w[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+  return v;
+}
+
+template <int KIND>
+__global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
+  using KT = KindTraits<KIND>;
+  using Op = MfmaOp<uint16_t, 32>;
+  constexpr int FM = 4, FN = 4;                   // 32 x 32 fragments per 128 x 128 wave tile
+  constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---------------- tile -> (expert, rows, columns) ----------------
+  int e = -1, row0 = 0, row_end = 0, k_len = 0;
+  const int n0 = blockIdx.y * BNH;
+  if (!KT::WGRAD) {
+    int acc_tiles = 0;
+    const int bx = blockIdx.x;
+    for (int i = 0; i < g.E; ++i) {
+      const int a = g.offsets[i], b = g.offsets[i + 1];
+      const int nt = (b - a + BM - 1) / BM;
+      if (bx < acc_tiles + nt) {
+        e = i;
+        row0 = a + (bx - acc_tiles) * BM;
+        row_end = b;
+        break;
+      }
+      acc_tiles += nt;
+    }
+    if (e < 0) return;
+    k_len = g.Kdim;
+  } else {
+    e = blockIdx.z;
+    row0 = blockIdx.x * BM;
+    row_end = g.Mdim;
+    k_len = g.offsets[e + 1] - g.offsets[e];
+  }
+  const int seg0 = KT::WGRAD ? g.offsets[e] : 0;
+
+  const uint16_t* A0 = (const uint16_t*)g.a0;
+  const uint16_t* A1 = (const uint16_t*)g.a1;
+  const uint16_t* B0 = (const uint16_t*)g.b0 + (KT::WGRAD ? 0 : (int64_t)e * g.b_estride);
+  const uint16_t* B1 = KT::DUAL_B || KT::DUAL_K ? (const uint16_t*)g.b1 + (KT::WGRAD ? 0 : (int64_t)e * g.b_estride)
+                                                : nullptr;
+  if (KT::WGRAD) {
+    A0 += (int64_t)seg0 * g.lda;
+    B0 += (int64_t)seg0 * g.ldb;
+    if (KT::DUAL_B) B1 += (int64_t)seg0 * g.ldb;
+  }
+  const int ktiles_half = (k_len + BK - 1) / BK;
+  const int ktiles = KT::DUAL_K ? 2 * ktiles_half : ktiles_half;
+  const int a_lim = KT::WGRAD ? g.Mdim : row_end;
+
+  auto issue = [&](int kt) {
+    char* st = lds + (kt % STAGES) * STAGE_BYTES;
+    const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
+    const int k0 = (kt - half * ktiles_half) * BK;
+    const uint16_t* A = half ? A1 : A0;
+    const uint16_t* B = half ? B1 : B0;
+    dma_tile<KT::A_MC>(st, A, nullptr, g.lda, row0, a_lim, k0, k_len, wave, lane);
+    dma_tile<KT::B_NC>(st + TILE_BYTES, B, KT::DUAL_B ? B1 : nullptr, g.ldb, n0, g.Ndim, k0, k_len, wave, lane);
+  };
+
+  Op::Acc acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < Op::kAcc; ++q) acc[i][j][q] = 0.f;
+
+  // B fragment j of this wave: first / second output half for dual-B
+  auto b_col = [&](int j) -> int {
+    if (KT::DUAL_B) return (j >> 1) * 128 + wn * 64 + (j & 1) * 32;
+    return wn * 128 + j * 32;
+  };
+
+#pragma unroll
+  for (int t = 0; t < STAGES - 1; ++t)
+    if (t < ktiles) issue(t);
+
+  for (int kt = 0; kt < ktiles; ++kt) {
+    // tile kt has landed once at most (tiles issued after it) x LOADS_PER_TILE remain
+    if (kt + 2 < ktiles) wait_vmcnt<2 * LOADS_PER_TILE>();
+    else if (kt + 1 < ktiles) wait_vmcnt<LOADS_PER_TILE>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // every thread's DMA for tile kt is visible; stage (kt-1) % STAGES is free
+    if (kt + STAGES - 1 < ktiles) issue(kt + STAGES - 1);
+    const char* At = lds + (kt % STAGES) * STAGE_BYTES;
+    const char* Bt = At + TILE_BYTES;
+    // fragments double-buffered in registers: step t+1 is read while step t's MFMAs run
+    Vec16 af[2][FM], bfr[2][FN];
+    auto read_frags = [&](int t, int slot) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[slot][i] = KT::A_MC ? frag_mc(At, wm * 128 + i * 32, t, lane) : frag_kc(At, wm * 128 + i * 32, t, lane);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[slot][j] = KT::B_NC ? frag_mc(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
+    };
+    read_frags(0, 0);
+#pragma unroll
+    for (int t = 0; t < BK / 16; ++t) {
+      if (t + 1 < BK / 16) read_frags(t + 1, (t + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) Op::run(acc[i][j], af[t & 1][i], bfr[t & 1][j]);
+    }
+  }
+  __syncthreads();  // all fragment reads done before the C tile overwrites the stages
+
+  // ---------------- epilogue (same contract as the generic kernel) ----------------
+  uint16_t* ctile = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < Op::kAcc; ++q)
+        ctile[(wm * 128 + i * 32 + Op::out_row(lane, q)) * LDC + b_col(j) + (lane & 31)] = f32_to_bf16(acc[i][j][q]);
+  __syncthreads();
+
+  constexpr int VEC = 8;
+  constexpr int CV = BNH / VEC;
+  const int rlim = KT::WGRAD ? g.Mdim : row_end;
+  for (int v = tid; v < BM * CV; v += NT) {
+    const int r = v / CV;
+    const int c = (v % CV) * VEC;
+    const int row = row0 + r;
+    const int col = n0 + c;
+    if (row >= rlim || col >= g.Ndim) continue;
+    const int64_t o = (int64_t)row * g.ldc + col;
+    const Vec16 c0 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + c);
+    if (KIND == kGateUpFwd) {
+      const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
+      Vec16 h;
+#pragma unroll
+      for (int t = 0; t < VEC; ++t) {
+        const float gv = VecTraits<uint16_t>::get(c0, t);
+        const float uv = VecTraits<uint16_t>::get(c1, t);
+        VecTraits<uint16_t>::set(h, t, round_to<uint16_t>(silu_f32(gv)) * uv);
+      }
+      if (g.c0) st16((uint16_t*)g.c0 + o, c0);
+      if (g.c1) st16((uint16_t*)g.c1 + o, c1);
+      st16((uint16_t*)g.c2 + o, h);
+    } else if (KIND == kDownDgrad) {
+      const Vec16 gi = ld16((const uint16_t*)g.x0 + o);
+      const Vec16 ui = ld16((const uint16_t*)g.x1 + o);
+      Vec16 dg, du;
+#pragma unroll
+      for (int t = 0; t < VEC; ++t) {
+        const float dh = VecTraits<uint16_t>::get(c0, t);
+        const float gv = VecTraits<uint16_t>::get(gi, t);
+        const float uv = VecTraits<uint16_t>::get(ui, t);
+        const float sig = sigmoid_f32(gv);
+        const float act = round_to<uint16_t>(silu_f32(gv));
+        const float dact = round_to<uint16_t>(dh * uv);
+        VecTraits<uint16_t>::set(dg, t, dact * sig * (1.0f + gv * (1.0f - sig)));
+        VecTraits<uint16_t>::set(du, t, dh * act);
+      }
+      st16((uint16_t*)g.c0 + o, dg);
+      st16((uint16_t*)g.c1 + o, du);
+    } else if (KIND == kGateUpWgrad) {
+      const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
+      const int64_t oe = (int64_t)e * g.c_estride + o;
+      st16((uint16_t*)g.c0 + oe, c0);
+      st16((uint16_t*)g.c1 + oe, c1);
+    } else {
+      st16((uint16_t*)g.c0 + (KT::WGRAD ? (int64_t)e * g.c_estride : 0) + o, c0);
+    }
+  }
+}
+
+}  // namespace pipe
+
+// Tile configuration per (dtype, kind).
+template <typename T, int KIND> struct Cfg;
+#ifndef ABACUS_BF16_CFG
+#define ABACUS_BF16_CFG 256, 256, 64, 2, 2, 32, 1
+#endif
+template <int KIND> struct Cfg<uint16_t, KIND> {
+  static constexpr int v[7] = {ABACUS_BF16_CFG};
+  static constexpr int BM = v[0], BN = v[1], BK = v[2], WM = v[3], WN = v[4], SHAPE = v[5], MINB = v[6];
+};
+template <int KIND> struct Cfg<float, KIND> {
+  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2, SHAPE = 16, MINB = 2;
+};
 
 template <typename T, int KIND>
 int launch_gemm(const GemmArgs& g, int R, hipStream_t s, const char* name) {
-  using C = Cfg<T>;
+  using C = Cfg<T, KIND>;
   using KT = KindTraits<KIND>;
   constexpr int BNH = KT::DUAL_B ? C::BN / 2 : C::BN;
   dim3 grid;
@@ -453,15 +759,41 @@ int launch_gemm(const GemmArgs& g, int R, hipStream_t s, const char* name) {
     grid = dim3((unsigned)((g.Mdim + C::BM - 1) / C::BM), (unsigned)((g.Ndim + BNH - 1) / BNH), (unsigned)g.E);
   }
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
-  hipLaunchKernelGGL((grouped_gemm_kernel<T, KIND, C::BM, C::BN, C::BK, C::WM, C::WN>), grid,
+  hipLaunchKernelGGL((grouped_gemm_kernel<T, KIND, C::BM, C::BN, C::BK, C::WM, C::WN, C::SHAPE, C::MINB>), grid,
                      dim3(C::WM * C::WN * 64), 0, s, g);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
 
 template <int KIND>
+int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
+  using KT = KindTraits<KIND>;
+  constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
+  dim3 grid;
+  if (!KT::WGRAD) {
+    const int64_t mt = (int64_t)(R + pipe::BM - 1) / pipe::BM + g.E;
+    grid = dim3((unsigned)mt, (unsigned)((g.Ndim + BNH - 1) / BNH), 1);
+  } else {
+    grid = dim3((unsigned)((g.Mdim + pipe::BM - 1) / pipe::BM), (unsigned)((g.Ndim + BNH - 1) / BNH), (unsigned)g.E);
+  }
+  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
+  hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, grid, dim3(pipe::NT), 0, s, g);
+  ABACUS_CHECK_LAUNCH(name);
+  return 0;
+}
+
+// bf16: the pipelined DMA kernel whenever every dimension it tiles is a
+// whole number of 16-byte chunks and the fixed reduction length is a whole
+// number of k-tiles (always true for the workloads; the generic kernel covers
+// the rest).  fp32: the generic kernel.
+template <int KIND>
 int dispatch_gemm(int dtype, const GemmArgs& g, int R, hipStream_t s, const char* name) {
-  if (dtype == kBF16) return launch_gemm<uint16_t, KIND>(g, R, s, name);
+  using KT = KindTraits<KIND>;
+  if (dtype == kBF16) {
+    const bool k_ok = KT::WGRAD || g.Kdim % pipe::BK == 0;
+    if (k_ok && g.Ndim % 8 == 0 && g.Mdim % 8 == 0) return launch_pipe<KIND>(g, R, s, name);
+    return launch_gemm<uint16_t, KIND>(g, R, s, name);
+  }
   return launch_gemm<float, KIND>(g, R, s, name);
 }
 
