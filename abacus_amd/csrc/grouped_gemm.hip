@@ -69,6 +69,7 @@ struct GemmArgs {
   int Mdim;                  // output rows: R (row-grouped) or the wgrad output rows
   int Ndim;                  // output columns (per half for DUAL_B)
   int Kdim;                  // reduction length (per half for DUAL_K); unused for WGRAD
+  int tiles_m, tiles_n;      // padded logical tile space of the pipelined kernel
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -462,12 +463,20 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_gemm_kernel(GemmArg
 // ===========================================================================
 namespace pipe {
 
-constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4, NT = 256;
+constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
+#ifndef ABACUS_PIPE_WAVES_N
+#define ABACUS_PIPE_WAVES_N 4
+#endif
+constexpr int WAVES_M = 2, WAVES_N = ABACUS_PIPE_WAVES_N;  // wave grid over the block tile
+constexpr int NWAVES = WAVES_M * WAVES_N, NT = NWAVES * 64;
+constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;     // wave tile
+constexpr int FM = WTM / 32, FN = WTN / 32;                // 32 x 32 fragments per wave
 constexpr int TILE_BYTES = 256 * BK * 2;          // one operand tile: 16 KB
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;       // A + B
 constexpr int LDC = BN + 8;                        // epilogue C tile row stride (bf16)
 constexpr int LDS_BYTES = STAGES * STAGE_BYTES > BM * LDC * 2 ? STAGES * STAGE_BYTES : BM * LDC * 2;
-constexpr int LOADS_PER_TILE = 8;                  // DMA instructions per thread per k-tile (A 4 + B 4)
+constexpr int DMA_PER_OPERAND = 1024 / NT;          // 16-byte chunks per thread per operand tile
+constexpr int LOADS_PER_TILE = 2 * DMA_PER_OPERAND; // DMA instructions per thread per k-tile
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -486,7 +495,16 @@ __device__ inline int mc_off(int k, int chunk) { return (k * 32 + (chunk ^ ((k &
 __device__ inline void dma16(const void* src, char* lds_dst) {
   const uint32_t lds_addr =
       __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_dst);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory", "m0");
+  // M0 is reserved by the compiler: save and restore it around the DMA.
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_addr)
+      : "memory");
 }
 
 // Wait until at most N DMA instructions of this thread are outstanding
@@ -498,7 +516,7 @@ __device__ inline void wait_vmcnt() {
 }
 
 // One operand tile -> LDS.  Chunk p of the tile (p = 0..1023) is written by
-// instruction i = p / 256 of wave (p / 64) % 4, lane p % 64.
+// instruction i = p / NT of wave (p / 64) % NWAVES, lane p % 64.
 //   kc: p -> (row = p / 4, chunk = swizzle^-1): element (row0 + row, k0 + 8 c)
 //   mc: p -> (k = p / 32, chunk):              element (k0 + k, mn0 + 8 c)
 // base1 != null splits the mn range in two halves of 128 (dual-B gate | up).
@@ -506,8 +524,8 @@ template <bool MC>
 __device__ inline void dma_tile(char* tile, const uint16_t* base0, const uint16_t* base1, int64_t ld, int r0,
                                 int r_lim, int k0, int k_lim, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int blk = i * 4 + wave;
+  for (int i = 0; i < DMA_PER_OPERAND; ++i) {
+    const int blk = i * NWAVES + wave;
     const int p = blk * 64 + lane;
     const void* src;
     if (!MC) {
@@ -555,25 +573,57 @@ __device__ inline Vec16 frag_mc(const char* tile, int f0, int t, int lane) {
   return v;
 }
 
+// XCD-aware tile order.  Work-groups are dispatched round-robin over the 8
+// XCDs (block b -> XCD b % 8), and each XCD has its own L2.  Block b is given
+// logical tile L = (b % 8) * (G / 8) + b / 8, so every XCD walks a contiguous
+// range of logical tiles; logical tiles are ordered in groups of GM row-tiles
+// x GN column-tiles (column fastest), so the ~32 blocks an XCD runs at once
+// share GM A-tiles and GN B-tiles through its L2 instead of each fetching
+// its own pair.  The logical space (per expert for wgrad) is padded to whole
+// groups; padding tiles exit.
+constexpr int GM = 8, GN = 4;
+
+struct TileId {
+  int e, mt, nt;
+};
+
+__host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+__device__ inline TileId tile_of_block(int b, int G, int MTp, int NTp) {
+  const int L = (b & 7) * (G >> 3) + (b >> 3);
+  const int per = MTp * NTp;
+  TileId t;
+  t.e = L / per;
+  const int l2 = L % per;
+  const int gi = l2 / (GM * GN), w = l2 % (GM * GN);
+  const int ngn = NTp / GN;
+  t.mt = (gi / ngn) * GM + w / GN;
+  t.nt = (gi % ngn) * GN + w % GN;
+  return t;
+}
+
 template <int KIND>
 __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   using KT = KindTraits<KIND>;
   using Op = MfmaOp<uint16_t, 32>;
-  constexpr int FM = 4, FN = 4;                   // 32 x 32 fragments per 128 x 128 wave tile
+  static_assert(!KindTraits<KIND>::DUAL_B || FN % 2 == 0, "dual-B pairs gate/up fragments");
   constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // ---------------- tile -> (expert, rows, columns) ----------------
+  // 1-D grid of G = (E or 1) x tiles_m x tiles_n blocks (a multiple of 8)
+  const TileId tl = tile_of_block(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n);
+  const int n0 = tl.nt * BNH;
+  if (n0 >= g.Ndim) return;
   int e = -1, row0 = 0, row_end = 0, k_len = 0;
-  const int n0 = blockIdx.y * BNH;
   if (!KT::WGRAD) {
     int acc_tiles = 0;
-    const int bx = blockIdx.x;
+    const int bx = tl.mt;
     for (int i = 0; i < g.E; ++i) {
       const int a = g.offsets[i], b = g.offsets[i + 1];
       const int nt = (b - a + BM - 1) / BM;
@@ -588,8 +638,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
     if (e < 0) return;
     k_len = g.Kdim;
   } else {
-    e = blockIdx.z;
-    row0 = blockIdx.x * BM;
+    e = tl.e;
+    row0 = tl.mt * BM;
+    if (e >= g.E || row0 >= g.Mdim) return;
     row_end = g.Mdim;
     k_len = g.offsets[e + 1] - g.offsets[e];
   }
@@ -627,10 +678,14 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < Op::kAcc; ++q) acc[i][j][q] = 0.f;
 
-  // B fragment j of this wave: first / second output half for dual-B
+  // B fragment j of this wave: dual-B waves hold matching gate (first half of
+  // the tile's columns) and up (second half) fragments
   auto b_col = [&](int j) -> int {
-    if (KT::DUAL_B) return (j >> 1) * 128 + wn * 64 + (j & 1) * 32;
-    return wn * 128 + j * 32;
+    if (KT::DUAL_B) {
+      constexpr int HF = FN / 2;
+      return (j / HF) * (BN / 2) + wn * HF * 32 + (j % HF) * 32;
+    }
+    return wn * WTN + j * 32;
   };
 
 #pragma unroll
@@ -651,7 +706,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
     auto read_frags = [&](int t, int slot) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        af[slot][i] = KT::A_MC ? frag_mc(At, wm * 128 + i * 32, t, lane) : frag_kc(At, wm * 128 + i * 32, t, lane);
+        af[slot][i] = KT::A_MC ? frag_mc(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         bfr[slot][j] = KT::B_NC ? frag_mc(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
@@ -676,7 +731,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
     for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int q = 0; q < Op::kAcc; ++q)
-        ctile[(wm * 128 + i * 32 + Op::out_row(lane, q)) * LDC + b_col(j) + (lane & 31)] = f32_to_bf16(acc[i][j][q]);
+        ctile[(wm * WTM + i * 32 + Op::out_row(lane, q)) * LDC + b_col(j) + (lane & 31)] = f32_to_bf16(acc[i][j][q]);
   __syncthreads();
 
   constexpr int VEC = 8;
@@ -769,15 +824,18 @@ template <int KIND>
 int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
   using KT = KindTraits<KIND>;
   constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
-  dim3 grid;
-  if (!KT::WGRAD) {
-    const int64_t mt = (int64_t)(R + pipe::BM - 1) / pipe::BM + g.E;
-    grid = dim3((unsigned)mt, (unsigned)((g.Ndim + BNH - 1) / BNH), 1);
-  } else {
-    grid = dim3((unsigned)((g.Mdim + pipe::BM - 1) / pipe::BM), (unsigned)((g.Ndim + BNH - 1) / BNH), (unsigned)g.E);
-  }
-  if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
-  hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, grid, dim3(pipe::NT), 0, s, g);
+  // padded logical tile space: MTp row tiles x NTp column tiles (x E for wgrad),
+  // whole GM x GN groups.
+  const int mt = KT::WGRAD ? (g.Mdim + pipe::BM - 1) / pipe::BM : (R + pipe::BM - 1) / pipe::BM + g.E;
+  const int nt = (g.Ndim + BNH - 1) / BNH;
+  const int MTp = pipe::round_up(mt, pipe::GM), NTp = pipe::round_up(nt, pipe::GN);
+  const int64_t total = (int64_t)(KT::WGRAD ? g.E : 1) * MTp * NTp;
+  if (mt == 0 || nt == 0) return 0;
+  ABACUS_CHECK_ARG(total < (1ll << 31), "%s: tile grid too large", name);
+  GemmArgs ga = g;
+  ga.tiles_m = MTp;
+  ga.tiles_n = NTp;
+  hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)total), dim3(pipe::NT), 0, s, ga);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
