@@ -463,7 +463,15 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_gemm_kernel(GemmArg
 // ===========================================================================
 namespace pipe {
 
-constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
+#ifndef ABACUS_PIPE_BK
+#define ABACUS_PIPE_BK 64
+#endif
+#ifndef ABACUS_PIPE_STAGES
+#define ABACUS_PIPE_STAGES 2
+#endif
+constexpr int BM = 256, BN = 256, BK = ABACUS_PIPE_BK, STAGES = ABACUS_PIPE_STAGES;
+constexpr int CPR = BK / 8;        // 16-byte chunks per k-contiguous LDS row
+static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
 #ifndef ABACUS_PIPE_WAVES_N
 #define ABACUS_PIPE_WAVES_N 4
 #endif
@@ -475,7 +483,8 @@ constexpr int TILE_BYTES = 256 * BK * 2;          // one operand tile: 16 KB
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;       // A + B
 constexpr int LDC = BN + 8;                        // epilogue C tile row stride (bf16)
 constexpr int LDS_BYTES = STAGES * STAGE_BYTES > BM * LDC * 2 ? STAGES * STAGE_BYTES : BM * LDC * 2;
-constexpr int DMA_PER_OPERAND = 1024 / NT;          // 16-byte chunks per thread per operand tile
+constexpr int TILE_CHUNKS = TILE_BYTES / 16;
+constexpr int DMA_PER_OPERAND = TILE_CHUNKS / NT;   // 16-byte chunks per thread per operand tile
 constexpr int LOADS_PER_TILE = 2 * DMA_PER_OPERAND; // DMA instructions per thread per k-tile
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -484,7 +493,9 @@ typedef __attribute__((address_space(3))) void lds_void;
 // 16 zero bytes: the DMA source for k beyond a ragged segment's end.
 __device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
 
-__device__ inline int kc_off(int row, int chunk) { return (row * 4 + (chunk ^ ((row >> 2) & 3))) * 16; }
+// kc rows are CPR chunks; 256 bytes of LDS banks hold 16 / CPR rows, so rows
+// of one bank period get distinct chunk permutations.
+__device__ inline int kc_off(int row, int chunk) { return (row * CPR + (chunk ^ ((row / (16 / CPR)) % CPR))) * 16; }
 __device__ inline int mc_off(int k, int chunk) { return (k * 32 + (chunk ^ ((k & 3) << 2))) * 16; }
 
 // global_load_lds_dwordx4 issued through inline asm: the compiler does not
@@ -515,43 +526,61 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
-// One operand tile -> LDS.  Chunk p of the tile (p = 0..1023) is written by
-// instruction i = p / NT of wave (p / 64) % NWAVES, lane p % 64.
-//   kc: p -> (row = p / 4, chunk = swizzle^-1): element (row0 + row, k0 + 8 c)
-//   mc: p -> (k = p / 32, chunk):              element (k0 + k, mn0 + 8 c)
-// base1 != null splits the mn range in two halves of 128 (dual-B gate | up).
+// One operand's DMA stream.  Chunk p of an operand tile (p = 0 .. TILE_CHUNKS-1)
+// is written by instruction i = p / NT of wave (p / 64) % NWAVES, lane p % 64:
+//   kc: p -> (row = p / CPR, chunk = swizzle^-1(p % CPR)): element (r0 + row, k0 + 8 c)
+//   mc: p -> (k = p / 32, chunk = swizzle^-1(p % 32)):    element (k0 + k, r0 + 8 c)
+// Everything but k0 is fixed for a tile, so setup() computes each lane's
+// source pointers once and issue() adds the k0 step (kc: k0 elements, mc:
+// k0 rows) -- one 64-bit add per DMA.  Chunks whose k lies beyond k_lim
+// (a ragged segment's tail) read the zero page instead.
 template <bool MC>
-__device__ inline void dma_tile(char* tile, const uint16_t* base0, const uint16_t* base1, int64_t ld, int r0,
-                                int r_lim, int k0, int k_lim, int wave, int lane) {
+struct DmaStream {
+  const uint16_t* base[DMA_PER_OPERAND];
+  int koff[DMA_PER_OPERAND];   // k of the chunk relative to k0
+  int64_t ld;
+
+  __device__ inline void setup(const uint16_t* b0, const uint16_t* b1, int64_t ld_, int r0, int r_lim, int wave,
+                               int lane) {
+    ld = ld_;
 #pragma unroll
-  for (int i = 0; i < DMA_PER_OPERAND; ++i) {
-    const int blk = i * NWAVES + wave;
-    const int p = blk * 64 + lane;
-    const void* src;
-    if (!MC) {
-      const int row = p >> 2;
-      const int c = (p & 3) ^ ((row >> 2) & 3);
-      int gr = r0 + row;
-      gr = gr < r_lim ? gr : r_lim - 1;
-      const int kk = k0 + c * 8;
-      src = kk < k_lim ? (const void*)(base0 + (int64_t)gr * ld + kk) : (const void*)g_zero16;
-    } else {
-      const int k = p >> 5;
-      const int c = (p & 31) ^ ((k & 3) << 2);
-      int mn = c * 8;
-      const uint16_t* b = base0;
-      if (base1 != nullptr && mn >= 128) {
-        b = base1;
-        mn -= 128;
+    for (int i = 0; i < DMA_PER_OPERAND; ++i) {
+      const int p = (i * NWAVES + wave) * 64 + lane;
+      if (!MC) {
+        const int row = p / CPR;
+        const int c = (p % CPR) ^ ((row / (16 / CPR)) % CPR);
+        int gr = r0 + row;
+        gr = gr < r_lim ? gr : r_lim - 1;
+        base[i] = b0 + (int64_t)gr * ld + c * 8;
+        koff[i] = c * 8;
+      } else {
+        const int k = p >> 5;
+        const int c = (p & 31) ^ ((k & 3) << 2);
+        int mn = c * 8;
+        const uint16_t* b = b0;
+        if (b1 != nullptr && mn >= BN / 2) {
+          b = b1;
+          mn -= BN / 2;
+        }
+        int gm = r0 + mn;
+        gm = gm < r_lim ? gm : r_lim - 8;
+        base[i] = b + (int64_t)k * ld + gm;
+        koff[i] = k;
       }
-      int gm = r0 + mn;
-      gm = gm < r_lim ? gm : r_lim - 8;
-      const int kk = k0 + k;
-      src = kk < k_lim ? (const void*)(b + (int64_t)kk * ld + gm) : (const void*)g_zero16;
     }
-    dma16(src, tile + blk * 1024);
   }
-}
+
+  // LDS destinations are wave-uniform: tile + (i * NWAVES + wave) * 1024.
+  template <bool RAGGED>
+  __device__ inline void issue(char* tile, int wave_u, int k0, int k_lim) const {
+#pragma unroll
+    for (int i = 0; i < DMA_PER_OPERAND; ++i) {
+      const void* src = MC ? (const void*)(base[i] + (int64_t)k0 * ld) : (const void*)(base[i] + k0);
+      if (RAGGED && k0 + koff[i] >= k_lim) src = (const void*)g_zero16;
+      dma16(src, tile + (i * NWAVES + wave_u) * 1024);
+    }
+  }
+};
 
 // 32 x 16 MFMA operand fragment (rows or columns f0 .. f0+31, k-step t of 2).
 __device__ inline Vec16 frag_kc(const char* tile, int f0, int t, int lane) {
@@ -660,14 +689,29 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   const int ktiles = KT::DUAL_K ? 2 * ktiles_half : ktiles_half;
   const int a_lim = KT::WGRAD ? g.Mdim : row_end;
 
+  // wave index as a scalar so the DMA destinations are computed in SGPRs
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  DmaStream<KT::A_MC> sa;
+  DmaStream<KT::B_NC> sb;
+  int half_set = 0;
+  sa.setup(A0, nullptr, g.lda, row0, a_lim, wave, lane);
+  sb.setup(B0, KT::DUAL_B ? B1 : nullptr, g.ldb, n0, g.Ndim, wave, lane);
   auto issue = [&](int kt) {
     char* st = lds + (kt % STAGES) * STAGE_BYTES;
     const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
+    if (KT::DUAL_K && half != half_set) {  // second half of the concatenated k range
+      sa.setup(A1, nullptr, g.lda, row0, a_lim, wave, lane);
+      sb.setup(B1, nullptr, g.ldb, n0, g.Ndim, wave, lane);
+      half_set = half;
+    }
     const int k0 = (kt - half * ktiles_half) * BK;
-    const uint16_t* A = half ? A1 : A0;
-    const uint16_t* B = half ? B1 : B0;
-    dma_tile<KT::A_MC>(st, A, nullptr, g.lda, row0, a_lim, k0, k_len, wave, lane);
-    dma_tile<KT::B_NC>(st + TILE_BYTES, B, KT::DUAL_B ? B1 : nullptr, g.ldb, n0, g.Ndim, k0, k_len, wave, lane);
+    if (KT::WGRAD && k0 + BK > k_len) {
+      sa.template issue<true>(st, wave_u, k0, k_len);
+      sb.template issue<true>(st + TILE_BYTES, wave_u, k0, k_len);
+    } else {
+      sa.template issue<false>(st, wave_u, k0, k_len);
+      sb.template issue<false>(st + TILE_BYTES, wave_u, k0, k_len);
+    }
   };
 
   Op::Acc acc[FM][FN];
@@ -694,9 +738,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
 
   for (int kt = 0; kt < ktiles; ++kt) {
     // tile kt has landed once at most (tiles issued after it) x LOADS_PER_TILE remain
-    if (kt + 2 < ktiles) wait_vmcnt<2 * LOADS_PER_TILE>();
-    else if (kt + 1 < ktiles) wait_vmcnt<LOADS_PER_TILE>();
-    else wait_vmcnt<0>();
+    {
+      const int later = min(STAGES - 2, ktiles - 1 - kt);  // tiles issued after kt so far
+      if (STAGES >= 4 && later >= 2) wait_vmcnt<(STAGES >= 4 ? 2 : 0) * LOADS_PER_TILE>();
+      else if (STAGES >= 3 && later >= 1) wait_vmcnt<(STAGES >= 3 ? 1 : 0) * LOADS_PER_TILE>();
+      else wait_vmcnt<0>();
+    }
     __syncthreads();  // every thread's DMA for tile kt is visible; stage (kt-1) % STAGES is free
     if (kt + STAGES - 1 < ktiles) issue(kt + STAGES - 1);
     const char* At = lds + (kt % STAGES) * STAGE_BYTES;
@@ -766,8 +813,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
         const float dh = VecTraits<uint16_t>::get(c0, t);
         const float gv = VecTraits<uint16_t>::get(gi, t);
         const float uv = VecTraits<uint16_t>::get(ui, t);
-        const float sig = sigmoid_f32(gv);
-        const float act = round_to<uint16_t>(silu_f32(gv));
+        const float den = 1.0f + expf(-gv);
+        const float sig = 1.0f / den;                   // sigmoid(g)
+        const float act = round_to<uint16_t>(gv / den); // silu(g) exactly as the forward computes it
         const float dact = round_to<uint16_t>(dh * uv);
         VecTraits<uint16_t>::set(dg, t, dact * sig * (1.0f + gv * (1.0f - sig)));
         VecTraits<uint16_t>::set(du, t, dh * act);
