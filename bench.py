@@ -50,6 +50,9 @@ def parse_args():
     p.add_argument("--workload", default="mixtral_bf16")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample duration")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="after the timed steps, copy 1 GiB device-to-device once (a known-size kernel "
+                        "to scale FETCH_SIZE / WRITE_SIZE counters against)")
     return p.parse_args()
 
 
@@ -65,6 +68,23 @@ def hbm_bytes(wl, name):
         return s * D * (T + 2 * R) + (s + 4 + 4 + 4) * R
     if name == "abacus_moe_unpermute_bwd":
         return s * D * (R + T) + (4 + 4 + 4) * R
+    return None
+
+
+TRAFFIC_FILE = "profiles/hbm_traffic_mixtral_bf16_fwd_bwd.md"
+
+
+def measured_traffic(name):
+    """HBM bytes per launch of an entry point from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
+                    return int(parts[2])
+    except OSError:
+        pass
     return None
 
 
@@ -165,6 +185,13 @@ def main():
     ms_per_step = 1000.0 * elapsed / args.steps
     tokens_per_s = wl.tokens / (ms_per_step / 1000.0)
 
+    if args.calibrate_copy:
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     totals = timer.totals_ms()
     R, D, M = wl.rows, wl.dim, wl.hidden
     peak_mfma = PEAK_BF16_TFLOPS if wl.dtype == torch.bfloat16 else PEAK_FP32_TFLOPS
@@ -187,8 +214,10 @@ def main():
     d_ms, d_n = totals[dominant]
     if dominant in GEMM_FLOPS:
         achieved = GEMM_FLOPS[dominant] * R * D * M / (d_ms / d_n / 1000.0) / 1e12
+        traffic = measured_traffic(dominant) if wl.name == "mixtral_bf16" else None
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak_mfma,
-                    "unit": "TFLOP/s", "frac": round(achieved / peak_mfma, 4), "traffic": None,
+                    "unit": "TFLOP/s", "frac": round(achieved / peak_mfma, 4), "traffic": traffic,
+                    "traffic_source": TRAFFIC_FILE if traffic is not None else None,
                     "algorithmic_per_launch": GEMM_FLOPS[dominant] * R * D * M}
     else:
         b = hbm_bytes(wl, dominant) or 0
