@@ -471,9 +471,10 @@ namespace pipe {
 #endif
 constexpr int BM = 256, BN = 256, BK = ABACUS_PIPE_BK, STAGES = ABACUS_PIPE_STAGES;
 constexpr int CPR = BK / 8;        // 16-byte chunks per k-contiguous LDS row
-static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
+static_assert(STAGES == 2, "the k-loop double-buffers LDS stages");
+constexpr int NSTEP = BK / 16;     // MFMA k-steps per k-tile
 #ifndef ABACUS_PIPE_WAVES_N
-#define ABACUS_PIPE_WAVES_N 4
+#define ABACUS_PIPE_WAVES_N 2
 #endif
 constexpr int WAVES_M = 2, WAVES_N = ABACUS_PIPE_WAVES_N;  // wave grid over the block tile
 constexpr int NWAVES = WAVES_M * WAVES_N, NT = NWAVES * 64;
@@ -526,6 +527,26 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
+// Wait until this thread's DMA and LDS reads have all completed.
+__device__ inline void wait_vm_lgkm_zero() { __builtin_amdgcn_s_waitcnt(7 << 4); }
+
+// Two floats to packed bf16 in one v_cvt_pk_bf16_f32: round to nearest even,
+// NaN made quiet -- bit-identical to f32_to_bf16 for every input.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ inline float lo_bf16(uint32_t w) { return bits_f32(w << 16); }
+__device__ inline float hi_bf16(uint32_t w) { return bits_f32(w & 0xffff0000u); }
+
+// 1 / (1 + exp(-x)) from the hardware exp2 and reciprocal (a few ulp in fp32,
+// far below the bf16 rounding of every value it feeds).  The forward SiLU and
+// its recomputation in the down-projection backward both use it, so the two
+// agree bit for bit.
+__device__ inline float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
 // One operand's DMA stream.  Chunk p of an operand tile (p = 0 .. TILE_CHUNKS-1)
 // is written by instruction i = p / NT of wave (p / 64) % NWAVES, lane p % 64:
 //   kc: p -> (row = p / CPR, chunk = swizzle^-1(p % CPR)): element (r0 + row, k0 + 8 c)
@@ -570,15 +591,13 @@ struct DmaStream {
     }
   }
 
-  // LDS destinations are wave-uniform: tile + (i * NWAVES + wave) * 1024.
-  template <bool RAGGED>
-  __device__ inline void issue(char* tile, int wave_u, int k0, int k_lim) const {
-#pragma unroll
-    for (int i = 0; i < DMA_PER_OPERAND; ++i) {
-      const void* src = MC ? (const void*)(base[i] + (int64_t)k0 * ld) : (const void*)(base[i] + k0);
-      if (RAGGED && k0 + koff[i] >= k_lim) src = (const void*)g_zero16;
-      dma16(src, tile + (i * NWAVES + wave_u) * 1024);
-    }
+  // Instruction i of this operand's k-tile at k0.  LDS destinations are
+  // wave-uniform: tile + (i * NWAVES + wave) * 1024.
+  template <bool MAYBE_RAGGED>
+  __device__ inline void issue_one(int i, char* tile, int wave_u, int k0, int k_lim) const {
+    const void* src = MC ? (const void*)(base[i] + (int64_t)k0 * ld) : (const void*)(base[i] + k0);
+    if (MAYBE_RAGGED && k0 + koff[i] >= k_lim) src = (const void*)g_zero16;
+    dma16(src, tile + (i * NWAVES + wave_u) * 1024);
   }
 };
 
@@ -696,22 +715,24 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   int half_set = 0;
   sa.setup(A0, nullptr, g.lda, row0, a_lim, wave, lane);
   sb.setup(B0, KT::DUAL_B ? B1 : nullptr, g.ldb, n0, g.Ndim, wave, lane);
-  auto issue = [&](int kt) {
-    char* st = lds + (kt % STAGES) * STAGE_BYTES;
+  // DMA of k-tile kt: prep(kt) resolves the stage, the k offset and (dual-K)
+  // the operand half once; dma(n) sends instruction n of LOADS_PER_TILE (A's
+  // first), so the k-loop can place each one between two MFMAs.
+  char* dma_stage = lds;
+  int dma_k0 = 0;
+  auto prep = [&](int kt) __attribute__((always_inline)) {
+    dma_stage = lds + (kt & 1) * STAGE_BYTES;
     const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
     if (KT::DUAL_K && half != half_set) {  // second half of the concatenated k range
       sa.setup(A1, nullptr, g.lda, row0, a_lim, wave, lane);
       sb.setup(B1, nullptr, g.ldb, n0, g.Ndim, wave, lane);
       half_set = half;
     }
-    const int k0 = (kt - half * ktiles_half) * BK;
-    if (KT::WGRAD && k0 + BK > k_len) {
-      sa.template issue<true>(st, wave_u, k0, k_len);
-      sb.template issue<true>(st + TILE_BYTES, wave_u, k0, k_len);
-    } else {
-      sa.template issue<false>(st, wave_u, k0, k_len);
-      sb.template issue<false>(st + TILE_BYTES, wave_u, k0, k_len);
-    }
+    dma_k0 = (kt - half * ktiles_half) * BK;
+  };
+  auto dma = [&](int n) __attribute__((always_inline)) {
+    if (n < DMA_PER_OPERAND) sa.template issue_one<KT::WGRAD>(n, dma_stage, wave_u, dma_k0, k_len);
+    else sb.template issue_one<KT::WGRAD>(n - DMA_PER_OPERAND, dma_stage + TILE_BYTES, wave_u, dma_k0, k_len);
   };
 
   Op::Acc acc[FM][FN];
@@ -724,7 +745,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
 
   // B fragment j of this wave: dual-B waves hold matching gate (first half of
   // the tile's columns) and up (second half) fragments
-  auto b_col = [&](int j) -> int {
+  auto b_col = [&](int j) __attribute__((always_inline)) -> int {
     if (KT::DUAL_B) {
       constexpr int HF = FN / 2;
       return (j / HF) * (BN / 2) + wn * HF * 32 + (j % HF) * 32;
@@ -732,103 +753,181 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
     return wn * WTN + j * 32;
   };
 
-#pragma unroll
-  for (int t = 0; t < STAGES - 1; ++t)
-    if (t < ktiles) issue(t);
+  // Fragments are double-buffered in registers (slot = step & 1).  Fragment f
+  // of a step is read in the order the MFMAs consume them: A0, B0..B(FN-1),
+  // A1..A(FM-1).
+  Vec16 af[2][FM], bfr[2][FN];
+  constexpr int NFRAG = FM + FN;
+  auto read_frag = [&](const char* st, int t, int slot, int f) __attribute__((always_inline)) {
+    const char* At = st;
+    const char* Bt = st + TILE_BYTES;
+    if (f == 0 || f > FN) {
+      const int i = f == 0 ? 0 : f - FN;
+      af[slot][i] = KT::A_MC ? frag_mc(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
+    } else {
+      const int j = f - 1;
+      bfr[slot][j] = KT::B_NC ? frag_mc(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
+    }
+  };
 
-  for (int kt = 0; kt < ktiles; ++kt) {
-    // tile kt has landed once at most (tiles issued after it) x LOADS_PER_TILE remain
-    {
-      const int later = min(STAGES - 2, ktiles - 1 - kt);  // tiles issued after kt so far
-      if (STAGES >= 4 && later >= 2) wait_vmcnt<(STAGES >= 4 ? 2 : 0) * LOADS_PER_TILE>();
-      else if (STAGES >= 3 && later >= 1) wait_vmcnt<(STAGES >= 3 ? 1 : 0) * LOADS_PER_TILE>();
-      else wait_vmcnt<0>();
+  // One k-step: the FM x FN MFMAs on fragment slot `slot`.  Fragment read f
+  // of the next step (from stage rd_st, step rd_t, into slot rd_slot) follows
+  // MFMA f; when `with_dma`, DMA instruction m follows MFMA m.  Each group is
+  // fenced with sched_barrier so the interleave survives scheduling: with one
+  // wave per SIMD, nothing else keeps the matrix core busy while this wave
+  // waits on LDS or issues loads.
+  auto kstep = [&](int slot, bool with_read, const char* rd_st, int rd_t, int rd_slot, bool with_dma) __attribute__((always_inline)) {
+    static_assert(FM * FN >= NFRAG && FM * FN >= LOADS_PER_TILE, "one read and one DMA per MFMA at most");
+#pragma unroll
+    for (int m = 0; m < FM * FN; ++m) {
+      // operands swapped: the fragment is C^T, so each lane ends up holding
+      // runs of 4 consecutive columns of one row (see the epilogue)
+      Op::run(acc[m / FN][m % FN], bfr[slot][m % FN], af[slot][m / FN]);
+      if (with_read && m < NFRAG) read_frag(rd_st, rd_t, rd_slot, m);
+      if (with_dma && m < LOADS_PER_TILE) dma(m);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();  // every thread's DMA for tile kt is visible; stage (kt-1) % STAGES is free
-    if (kt + STAGES - 1 < ktiles) issue(kt + STAGES - 1);
-    const char* At = lds + (kt % STAGES) * STAGE_BYTES;
-    const char* Bt = At + TILE_BYTES;
-    // fragments double-buffered in registers: step t+1 is read while step t's MFMAs run
-    Vec16 af[2][FM], bfr[2][FN];
-    auto read_frags = [&](int t, int slot) {
+  };
+
+  // One k-tile.  Steps 0..NSTEP-2 read the next step's fragments from this
+  // stage.  Before the last step, one barrier: every wave has its reads of
+  // this stage back (so the stage can be refilled) and has seen its DMA of
+  // tile kt+1 land (so that tile can be read).  The last step's MFMAs then
+  // cover the first reads of tile kt+1 and the DMA of tile kt+2 into this
+  // stage.
+  auto ktile = [&](int kt, bool next, bool dma_next) __attribute__((always_inline)) {
+    char* st = lds + (kt & 1) * STAGE_BYTES;
+    char* st_next = lds + ((kt + 1) & 1) * STAGE_BYTES;
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[slot][i] = KT::A_MC ? frag_mc(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
+    for (int t = 0; t < NSTEP - 1; ++t) kstep(t & 1, true, st, t + 1, (t + 1) & 1, false);
+    wait_vm_lgkm_zero();
+    __syncthreads();
+    if (dma_next) prep(kt + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    kstep((NSTEP - 1) & 1, next, st_next, 0, 0, dma_next);
+  };
+
+  // prologue: tiles 0 and 1 in flight, tile 0's first fragments read.  A
+  // tile with no k range (an empty wgrad segment) keeps zero accumulators.
+  if (ktiles > 0) {
+  prep(0);
 #pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bfr[slot][j] = KT::B_NC ? frag_mc(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
-    };
-    read_frags(0, 0);
+  for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
+  if (ktiles > 1) {
+    prep(1);
 #pragma unroll
-    for (int t = 0; t < BK / 16; ++t) {
-      if (t + 1 < BK / 16) read_frags(t + 1, (t + 1) & 1);
+    for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
+    wait_vmcnt<LOADS_PER_TILE>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  __syncthreads();
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) Op::run(acc[i][j], af[t & 1][i], bfr[t & 1][j]);
-    }
+  for (int f = 0; f < NFRAG; ++f) read_frag(lds, 0, 0, f);
+
+  // steady state, then the last two tiles (no DMA; no next tile for the last)
+  int kt = 0;
+  for (; kt + 2 < ktiles; ++kt) ktile(kt, true, true);
+  if (kt + 1 < ktiles) ktile(kt++, true, false);
+  ktile(kt, false, false);
   }
   __syncthreads();  // all fragment reads done before the C tile overwrites the stages
 
   // ---------------- epilogue (same contract as the generic kernel) ----------------
+  // Fragment (i, j) holds C^T: lane l has row (l & 31) of the fragment and, for
+  // g = 0..3, columns 8g + 4 (l >> 5) .. +3.  Each such run goes to the
+  // row-major C tile as one 8-byte write of packed bf16 (with LDC = BN + 8 the
+  // 64 lanes cover every LDS bank twice: no conflicts).
   uint16_t* ctile = reinterpret_cast<uint16_t*>(lds);
+  {
+    const int rl = lane & 31, ch = 4 * (lane >> 5);
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+      for (int j = 0; j < FN; ++j)
 #pragma unroll
-      for (int q = 0; q < Op::kAcc; ++q)
-        ctile[(wm * WTM + i * 32 + Op::out_row(lane, q)) * LDC + b_col(j) + (lane & 31)] = f32_to_bf16(acc[i][j][q]);
+        for (int gq = 0; gq < 4; ++gq) {
+          uint2 w;
+          w.x = pack_bf16x2(acc[i][j][4 * gq], acc[i][j][4 * gq + 1]);
+          w.y = pack_bf16x2(acc[i][j][4 * gq + 2], acc[i][j][4 * gq + 3]);
+          *reinterpret_cast<uint2*>(ctile + (wm * WTM + i * 32 + rl) * LDC + b_col(j) + 8 * gq + ch) = w;
+        }
+  }
   __syncthreads();
 
+  // C tile -> global, 8 columns per vector, in batches whose global loads (the
+  // down-projection backward reads G and U) are all in flight before any of
+  // the batch is computed.
   constexpr int VEC = 8;
   constexpr int CV = BNH / VEC;
+  constexpr int NV = BM * CV / NT;  // vectors per thread
+  constexpr int BATCH = 8;
+  static_assert(NV % BATCH == 0, "whole batches");
   const int rlim = KT::WGRAD ? g.Mdim : row_end;
-  for (int v = tid; v < BM * CV; v += NT) {
-    const int r = v / CV;
-    const int c = (v % CV) * VEC;
-    const int row = row0 + r;
-    const int col = n0 + c;
-    if (row >= rlim || col >= g.Ndim) continue;
-    const int64_t o = (int64_t)row * g.ldc + col;
-    const Vec16 c0 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + c);
-    if (KIND == kGateUpFwd) {
-      const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
-      Vec16 h;
+#pragma unroll 1
+  for (int b0 = 0; b0 < NV; b0 += BATCH) {
+    Vec16 xg[BATCH], xu[BATCH];
+    if (KIND == kDownDgrad) {
 #pragma unroll
-      for (int t = 0; t < VEC; ++t) {
-        const float gv = VecTraits<uint16_t>::get(c0, t);
-        const float uv = VecTraits<uint16_t>::get(c1, t);
-        VecTraits<uint16_t>::set(h, t, round_to<uint16_t>(silu_f32(gv)) * uv);
+      for (int u = 0; u < BATCH; ++u) {
+        const int v = tid + (b0 + u) * NT;
+        const int row = row0 + v / CV, col = n0 + (v % CV) * VEC;
+        if (row < rlim && col < g.Ndim) {
+          const int64_t o = (int64_t)row * g.ldc + col;
+          xg[u] = ld16((const uint16_t*)g.x0 + o);
+          xu[u] = ld16((const uint16_t*)g.x1 + o);
+        }
       }
-      if (g.c0) st16((uint16_t*)g.c0 + o, c0);
-      if (g.c1) st16((uint16_t*)g.c1 + o, c1);
-      st16((uint16_t*)g.c2 + o, h);
-    } else if (KIND == kDownDgrad) {
-      const Vec16 gi = ld16((const uint16_t*)g.x0 + o);
-      const Vec16 ui = ld16((const uint16_t*)g.x1 + o);
-      Vec16 dg, du;
+    }
 #pragma unroll
-      for (int t = 0; t < VEC; ++t) {
-        const float dh = VecTraits<uint16_t>::get(c0, t);
-        const float gv = VecTraits<uint16_t>::get(gi, t);
-        const float uv = VecTraits<uint16_t>::get(ui, t);
-        const float den = 1.0f + expf(-gv);
-        const float sig = 1.0f / den;                   // sigmoid(g)
-        const float act = round_to<uint16_t>(gv / den); // silu(g) exactly as the forward computes it
-        const float dact = round_to<uint16_t>(dh * uv);
-        VecTraits<uint16_t>::set(dg, t, dact * sig * (1.0f + gv * (1.0f - sig)));
-        VecTraits<uint16_t>::set(du, t, dh * act);
+    for (int u = 0; u < BATCH; ++u) {
+      const int v = tid + (b0 + u) * NT;
+      const int r = v / CV;
+      const int c = (v % CV) * VEC;
+      const int row = row0 + r;
+      const int col = n0 + c;
+      if (row >= rlim || col >= g.Ndim) continue;
+      const int64_t o = (int64_t)row * g.ldc + col;
+      const Vec16 c0 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + c);
+      if (KIND == kGateUpFwd) {
+        // H = bf16(bf16(silu(G)) * U) on the bf16-rounded G and U
+        const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
+        Vec16 h;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float g0 = lo_bf16(c0.w[w]), g1 = hi_bf16(c0.w[w]);
+          const uint32_t act = pack_bf16x2(g0 * sigmoid_hw(g0), g1 * sigmoid_hw(g1));
+          h.w[w] = pack_bf16x2(lo_bf16(act) * lo_bf16(c1.w[w]), hi_bf16(act) * hi_bf16(c1.w[w]));
+        }
+        if (g.c0) st16((uint16_t*)g.c0 + o, c0);
+        if (g.c1) st16((uint16_t*)g.c1 + o, c1);
+        st16((uint16_t*)g.c2 + o, h);
+      } else if (KIND == kDownDgrad) {
+        // dH -> dG, dU through H = silu(G) * U, each product rounded as the
+        // forward rounds it: dact = bf16(dH * U), act = bf16(silu(G))
+        Vec16 dg, du;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          float dh[2] = {lo_bf16(c0.w[w]), hi_bf16(c0.w[w])};
+          float gv[2] = {lo_bf16(xg[u].w[w]), hi_bf16(xg[u].w[w])};
+          float uv[2] = {lo_bf16(xu[u].w[w]), hi_bf16(xu[u].w[w])};
+          const float sig0 = sigmoid_hw(gv[0]), sig1 = sigmoid_hw(gv[1]);
+          const uint32_t act = pack_bf16x2(gv[0] * sig0, gv[1] * sig1);
+          const uint32_t dact = pack_bf16x2(dh[0] * uv[0], dh[1] * uv[1]);
+          dg.w[w] = pack_bf16x2(lo_bf16(dact) * sig0 * (1.0f + gv[0] * (1.0f - sig0)),
+                                hi_bf16(dact) * sig1 * (1.0f + gv[1] * (1.0f - sig1)));
+          du.w[w] = pack_bf16x2(dh[0] * lo_bf16(act), dh[1] * hi_bf16(act));
+        }
+        st16((uint16_t*)g.c0 + o, dg);
+        st16((uint16_t*)g.c1 + o, du);
+      } else if (KIND == kGateUpWgrad) {
+        const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
+        const int64_t oe = (int64_t)e * g.c_estride + o;
+        st16((uint16_t*)g.c0 + oe, c0);
+        st16((uint16_t*)g.c1 + oe, c1);
+      } else {
+        st16((uint16_t*)g.c0 + (KT::WGRAD ? (int64_t)e * g.c_estride : 0) + o, c0);
       }
-      st16((uint16_t*)g.c0 + o, dg);
-      st16((uint16_t*)g.c1 + o, du);
-    } else if (KIND == kGateUpWgrad) {
-      const Vec16 c1 = *reinterpret_cast<const Vec16*>(ctile + r * LDC + BN / 2 + c);
-      const int64_t oe = (int64_t)e * g.c_estride + o;
-      st16((uint16_t*)g.c0 + oe, c0);
-      st16((uint16_t*)g.c1 + oe, c1);
-    } else {
-      st16((uint16_t*)g.c0 + (KT::WGRAD ? (int64_t)e * g.c_estride : 0) + o, c0);
     }
   }
 }
