@@ -471,7 +471,7 @@ namespace pipe {
 #endif
 constexpr int BM = 256, BN = 256, BK = ABACUS_PIPE_BK, STAGES = ABACUS_PIPE_STAGES;
 constexpr int CPR = BK / 8;        // 16-byte chunks per k-contiguous LDS row
-static_assert(STAGES == 2, "the k-loop double-buffers LDS stages");
+static_assert(STAGES >= 2 && STAGES <= 5, "2..5 LDS stages");
 constexpr int NSTEP = BK / 16;     // MFMA k-steps per k-tile
 #ifndef ABACUS_PIPE_WAVES_N
 #define ABACUS_PIPE_WAVES_N 2
@@ -484,6 +484,7 @@ constexpr int TILE_BYTES = 256 * BK * 2;          // one operand tile: 16 KB
 constexpr int STAGE_BYTES = 2 * TILE_BYTES;       // A + B
 constexpr int LDC = BN + 8;                        // epilogue C tile row stride (bf16)
 constexpr int LDS_BYTES = STAGES * STAGE_BYTES > BM * LDC * 2 ? STAGES * STAGE_BYTES : BM * LDC * 2;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS is 160 KB per work-group");
 constexpr int TILE_CHUNKS = TILE_BYTES / 16;
 constexpr int DMA_PER_OPERAND = TILE_CHUNKS / NT;   // 16-byte chunks per thread per operand tile
 constexpr int LOADS_PER_TILE = 2 * DMA_PER_OPERAND; // DMA instructions per thread per k-tile
@@ -526,9 +527,6 @@ __device__ inline void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
-
-// Wait until this thread's DMA and LDS reads have all completed.
-__device__ inline void wait_vm_lgkm_zero() { __builtin_amdgcn_s_waitcnt(7 << 4); }
 
 // Two floats to packed bf16 in one v_cvt_pk_bf16_f32: round to nearest even,
 // NaN made quiet -- bit-identical to f32_to_bf16 for every input.
@@ -650,13 +648,15 @@ __device__ inline TileId tile_of_block(int b, int G, int MTp, int NTp) {
   return t;
 }
 
+// One 256 x 256 output tile of a GEMM kind: block b of the kind's G blocks
+// (G a multiple of 8, so b % 8 is still the XCD the block runs on when a
+// launch runs several kinds back to back).  lds: the work-group's LDS_BYTES.
 template <int KIND>
-__global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
+__device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& g, int b, int G, char* lds) {
   using KT = KindTraits<KIND>;
   using Op = MfmaOp<uint16_t, 32>;
   static_assert(!KindTraits<KIND>::DUAL_B || FN % 2 == 0, "dual-B pairs gate/up fragments");
   constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -664,8 +664,8 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // ---------------- tile -> (expert, rows, columns) ----------------
-  // 1-D grid of G = (E or 1) x tiles_m x tiles_n blocks (a multiple of 8)
-  const TileId tl = tile_of_block(blockIdx.x, gridDim.x, g.tiles_m, g.tiles_n);
+  // 1-D space of G = (E or 1) x tiles_m x tiles_n blocks
+  const TileId tl = tile_of_block(b, G, g.tiles_m, g.tiles_n);
   const int n0 = tl.nt * BNH;
   if (n0 >= g.Ndim) return;
   int e = -1, row0 = 0, row_end = 0, k_len = 0;
@@ -721,7 +721,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   char* dma_stage = lds;
   int dma_k0 = 0;
   auto prep = [&](int kt) __attribute__((always_inline)) {
-    dma_stage = lds + (kt & 1) * STAGE_BYTES;
+    dma_stage = lds + (kt % STAGES) * STAGE_BYTES;
     const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
     if (KT::DUAL_K && half != half_set) {  // second half of the concatenated k range
       sa.setup(A1, nullptr, g.lda, row0, a_lim, wave, lane);
@@ -789,51 +789,92 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
     }
   };
 
+  // Wait until tile kt+1 has landed: `later` tiles were issued after it.
+  auto wait_next = [&](int later) __attribute__((always_inline)) {
+    if (STAGES >= 5 && later >= 3) wait_vmcnt<(STAGES >= 5 ? 3 : 0) * LOADS_PER_TILE>();
+    else if (STAGES >= 4 && later >= 2) wait_vmcnt<(STAGES >= 4 ? 2 : 0) * LOADS_PER_TILE>();
+    else if (STAGES >= 3 && later >= 1) wait_vmcnt<(STAGES >= 3 ? 1 : 0) * LOADS_PER_TILE>();
+    else wait_vmcnt<0>();
+  };
+
   // One k-tile.  Steps 0..NSTEP-2 read the next step's fragments from this
   // stage.  Before the last step, one barrier: every wave has its reads of
   // this stage back (so the stage can be refilled) and has seen its DMA of
   // tile kt+1 land (so that tile can be read).  The last step's MFMAs then
-  // cover the first reads of tile kt+1 and the DMA of tile kt+2 into this
-  // stage.
+  // cover the first reads of tile kt+1 and the DMA of tile kt+STAGES into
+  // this stage.
   auto ktile = [&](int kt, bool next, bool dma_next) __attribute__((always_inline)) {
-    char* st = lds + (kt & 1) * STAGE_BYTES;
-    char* st_next = lds + ((kt + 1) & 1) * STAGE_BYTES;
+    char* st = lds + (kt % STAGES) * STAGE_BYTES;
+    char* st_next = lds + ((kt + 1) % STAGES) * STAGE_BYTES;
 #pragma unroll
     for (int t = 0; t < NSTEP - 1; ++t) kstep(t & 1, true, st, t + 1, (t + 1) & 1, false);
-    wait_vm_lgkm_zero();
+    // tiles kt+2 .. min(kt+STAGES-1, ktiles-1) may still be in flight
+    wait_next(min(STAGES - 2, ktiles - 2 - kt));
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of the stage are back
     __syncthreads();
-    if (dma_next) prep(kt + 2);
+    if (dma_next) prep(kt + STAGES);
     __builtin_amdgcn_sched_barrier(0);
     kstep((NSTEP - 1) & 1, next, st_next, 0, 0, dma_next);
   };
 
-  // prologue: tiles 0 and 1 in flight, tile 0's first fragments read.  A
-  // tile with no k range (an empty wgrad segment) keeps zero accumulators.
+  // prologue: tiles 0 .. STAGES-1 in flight, tile 0's first fragments read.
+  // A tile with no k range (an empty wgrad segment) keeps zero accumulators.
   if (ktiles > 0) {
-  prep(0);
 #pragma unroll
-  for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
-  if (ktiles > 1) {
-    prep(1);
+    for (int p = 0; p < STAGES; ++p)
+      if (p < ktiles) {
+        prep(p);
 #pragma unroll
-    for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
-    wait_vmcnt<LOADS_PER_TILE>();
-  } else {
-    wait_vmcnt<0>();
-  }
-  __syncthreads();
+        for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
+      }
+    // tile 0 landed: tiles 1 .. min(STAGES, ktiles) - 1 may be in flight
+    {
+      const int later = min(STAGES, ktiles) - 1;
+      if (STAGES >= 5 && later >= 4) wait_vmcnt<(STAGES >= 5 ? 4 : 0) * LOADS_PER_TILE>();
+      else if (STAGES >= 4 && later >= 3) wait_vmcnt<(STAGES >= 4 ? 3 : 0) * LOADS_PER_TILE>();
+      else if (STAGES >= 3 && later >= 2) wait_vmcnt<(STAGES >= 3 ? 2 : 0) * LOADS_PER_TILE>();
+      else if (later >= 1) wait_vmcnt<LOADS_PER_TILE>();
+      else wait_vmcnt<0>();
+    }
+    __syncthreads();
 #pragma unroll
-  for (int f = 0; f < NFRAG; ++f) read_frag(lds, 0, 0, f);
+    for (int f = 0; f < NFRAG; ++f) read_frag(lds, 0, 0, f);
 
-  // steady state, then the last two tiles (no DMA; no next tile for the last)
-  int kt = 0;
-  for (; kt + 2 < ktiles; ++kt) ktile(kt, true, true);
-  if (kt + 1 < ktiles) ktile(kt++, true, false);
-  ktile(kt, false, false);
+    // steady state, then the last tiles (no DMA; no next tile for the last)
+    int kt = 0;
+    for (; kt + STAGES < ktiles; ++kt) ktile(kt, true, true);
+    for (; kt + 1 < ktiles; ++kt) ktile(kt, true, false);
+    ktile(kt, false, false);
   }
   __syncthreads();  // all fragment reads done before the C tile overwrites the stages
 
   // ---------------- epilogue (same contract as the generic kernel) ----------------
+  // C tile -> global goes 8 columns per vector, NV vectors per thread, in
+  // batches.  The down-projection backward also reads G and U there: those
+  // loads are double-buffered per batch and the first batch is issued before
+  // the C tile is staged, so HBM latency is paid about once per tile.
+  constexpr int VEC = 8;
+  constexpr int CV = BNH / VEC;
+  constexpr int NV = BM * CV / NT;  // vectors per thread
+  constexpr int BATCH = 8;
+  constexpr int NBATCH = NV / BATCH;
+  static_assert(NV % BATCH == 0, "whole batches");
+  const int rlim = KT::WGRAD ? g.Mdim : row_end;
+  Vec16 xg[2][BATCH], xu[2][BATCH];
+  auto load_gu = [&](int bi, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < BATCH; ++u) {
+      const int v = tid + (bi * BATCH + u) * NT;
+      const int row = row0 + v / CV, col = n0 + (v % CV) * VEC;
+      if (row < rlim && col < g.Ndim) {
+        const int64_t o = (int64_t)row * g.ldc + col;
+        xg[slot][u] = ld16((const uint16_t*)g.x0 + o);
+        xu[slot][u] = ld16((const uint16_t*)g.x1 + o);
+      }
+    }
+  };
+  if (KIND == kDownDgrad) load_gu(0, 0);
+
   // Fragment (i, j) holds C^T: lane l has row (l & 31) of the fragment and, for
   // g = 0..3, columns 8g + 4 (l >> 5) .. +3.  Each such run goes to the
   // row-major C tile as one 8-byte write of packed bf16 (with LDC = BN + 8 the
@@ -855,33 +896,12 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   }
   __syncthreads();
 
-  // C tile -> global, 8 columns per vector, in batches whose global loads (the
-  // down-projection backward reads G and U) are all in flight before any of
-  // the batch is computed.
-  constexpr int VEC = 8;
-  constexpr int CV = BNH / VEC;
-  constexpr int NV = BM * CV / NT;  // vectors per thread
-  constexpr int BATCH = 8;
-  static_assert(NV % BATCH == 0, "whole batches");
-  const int rlim = KT::WGRAD ? g.Mdim : row_end;
-#pragma unroll 1
-  for (int b0 = 0; b0 < NV; b0 += BATCH) {
-    Vec16 xg[BATCH], xu[BATCH];
-    if (KIND == kDownDgrad) {
 #pragma unroll
-      for (int u = 0; u < BATCH; ++u) {
-        const int v = tid + (b0 + u) * NT;
-        const int row = row0 + v / CV, col = n0 + (v % CV) * VEC;
-        if (row < rlim && col < g.Ndim) {
-          const int64_t o = (int64_t)row * g.ldc + col;
-          xg[u] = ld16((const uint16_t*)g.x0 + o);
-          xu[u] = ld16((const uint16_t*)g.x1 + o);
-        }
-      }
-    }
+  for (int bi = 0; bi < NBATCH; ++bi) {
+    if (KIND == kDownDgrad && bi + 1 < NBATCH) load_gu(bi + 1, (bi + 1) & 1);
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
-      const int v = tid + (b0 + u) * NT;
+      const int v = tid + (bi * BATCH + u) * NT;
       const int r = v / CV;
       const int c = (v % CV) * VEC;
       const int row = row0 + r;
@@ -905,18 +925,19 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
       } else if (KIND == kDownDgrad) {
         // dH -> dG, dU through H = silu(G) * U, each product rounded as the
         // forward rounds it: dact = bf16(dH * U), act = bf16(silu(G))
+        const Vec16& gi = xg[bi & 1][u];
+        const Vec16& ui = xu[bi & 1][u];
         Vec16 dg, du;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-          float dh[2] = {lo_bf16(c0.w[w]), hi_bf16(c0.w[w])};
-          float gv[2] = {lo_bf16(xg[u].w[w]), hi_bf16(xg[u].w[w])};
-          float uv[2] = {lo_bf16(xu[u].w[w]), hi_bf16(xu[u].w[w])};
-          const float sig0 = sigmoid_hw(gv[0]), sig1 = sigmoid_hw(gv[1]);
-          const uint32_t act = pack_bf16x2(gv[0] * sig0, gv[1] * sig1);
-          const uint32_t dact = pack_bf16x2(dh[0] * uv[0], dh[1] * uv[1]);
-          dg.w[w] = pack_bf16x2(lo_bf16(dact) * sig0 * (1.0f + gv[0] * (1.0f - sig0)),
-                                hi_bf16(dact) * sig1 * (1.0f + gv[1] * (1.0f - sig1)));
-          du.w[w] = pack_bf16x2(dh[0] * lo_bf16(act), dh[1] * hi_bf16(act));
+          const float dh0 = lo_bf16(c0.w[w]), dh1 = hi_bf16(c0.w[w]);
+          const float g0 = lo_bf16(gi.w[w]), g1 = hi_bf16(gi.w[w]);
+          const float sig0 = sigmoid_hw(g0), sig1 = sigmoid_hw(g1);
+          const uint32_t act = pack_bf16x2(g0 * sig0, g1 * sig1);
+          const uint32_t dact = pack_bf16x2(dh0 * lo_bf16(ui.w[w]), dh1 * hi_bf16(ui.w[w]));
+          dg.w[w] = pack_bf16x2(lo_bf16(dact) * sig0 * (1.0f + g0 * (1.0f - sig0)),
+                                hi_bf16(dact) * sig1 * (1.0f + g1 * (1.0f - sig1)));
+          du.w[w] = pack_bf16x2(dh0 * lo_bf16(act), dh1 * hi_bf16(act));
         }
         st16((uint16_t*)g.c0 + o, dg);
         st16((uint16_t*)g.c1 + o, du);
@@ -930,6 +951,24 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
       }
     }
   }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+  gemm_tile<KIND>(g, blockIdx.x, gridDim.x, lds);
+}
+
+// Two independent GEMMs in one launch: blocks [0, ga_blocks) run kind KA's
+// tiles, the rest kind KB's.  Blocks are dispatched in index order, so when KA
+// has the long tiles (a data gradient over the full reduction) and KB the
+// short ones (a weight gradient over one expert's rows), KB's tiles fill the
+// CUs that KA's last partial round of tiles would leave idle.
+template <int KA, int KB>
+__global__ __launch_bounds__(NT, 1) void gemm_bf16_pair_kernel(GemmArgs ga, GemmArgs gb, int ga_blocks) {
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+  if ((int)blockIdx.x < ga_blocks) gemm_tile<KA>(ga, blockIdx.x, ga_blocks, lds);
+  else gemm_tile<KB>(gb, (int)blockIdx.x - ga_blocks, (int)gridDim.x - ga_blocks, lds);
 }
 
 }  // namespace pipe
@@ -967,22 +1006,41 @@ int launch_gemm(const GemmArgs& g, int R, hipStream_t s, const char* name) {
   return 0;
 }
 
+// Sizes the padded logical tile space of a pipelined launch: MTp row tiles x
+// NTp column tiles (x E for wgrad), whole GM x GN groups.  Returns the number
+// of blocks (0: nothing to do).
 template <int KIND>
-int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
+int64_t pipe_grid(GemmArgs& g, int R) {
   using KT = KindTraits<KIND>;
   constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
-  // padded logical tile space: MTp row tiles x NTp column tiles (x E for wgrad),
-  // whole GM x GN groups.
   const int mt = KT::WGRAD ? (g.Mdim + pipe::BM - 1) / pipe::BM : (R + pipe::BM - 1) / pipe::BM + g.E;
   const int nt = (g.Ndim + BNH - 1) / BNH;
-  const int MTp = pipe::round_up(mt, pipe::GM), NTp = pipe::round_up(nt, pipe::GN);
-  const int64_t total = (int64_t)(KT::WGRAD ? g.E : 1) * MTp * NTp;
   if (mt == 0 || nt == 0) return 0;
-  ABACUS_CHECK_ARG(total < (1ll << 31), "%s: tile grid too large", name);
+  g.tiles_m = pipe::round_up(mt, pipe::GM);
+  g.tiles_n = pipe::round_up(nt, pipe::GN);
+  return (int64_t)(KT::WGRAD ? g.E : 1) * g.tiles_m * g.tiles_n;
+}
+
+template <int KIND>
+int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
   GemmArgs ga = g;
-  ga.tiles_m = MTp;
-  ga.tiles_n = NTp;
+  const int64_t total = pipe_grid<KIND>(ga, R);
+  if (total == 0) return 0;
+  ABACUS_CHECK_ARG(total < (1ll << 31), "%s: tile grid too large", name);
   hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)total), dim3(pipe::NT), 0, s, ga);
+  ABACUS_CHECK_LAUNCH(name);
+  return 0;
+}
+
+// Kinds KA (the long tiles) and KB in one launch.
+template <int KA, int KB>
+int launch_pipe_pair(const GemmArgs& a, int Ra, const GemmArgs& b, int Rb, hipStream_t s, const char* name) {
+  GemmArgs ga = a, gb = b;
+  const int64_t na = pipe_grid<KA>(ga, Ra), nb = pipe_grid<KB>(gb, Rb);
+  ABACUS_CHECK_ARG(na + nb < (1ll << 31), "%s: tile grid too large", name);
+  if (na + nb == 0) return 0;
+  hipLaunchKernelGGL((pipe::gemm_bf16_pair_kernel<KA, KB>), dim3((unsigned)(na + nb)), dim3(pipe::NT), 0, s, ga, gb,
+                     (int)na);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
@@ -992,14 +1050,28 @@ int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
 // number of k-tiles (always true for the workloads; the generic kernel covers
 // the rest).  fp32: the generic kernel.
 template <int KIND>
+bool pipe_ok(int dtype, const GemmArgs& g) {
+  return dtype == kBF16 && (KindTraits<KIND>::WGRAD || g.Kdim % pipe::BK == 0) && g.Ndim % 8 == 0 &&
+         g.Mdim % 8 == 0;
+}
+
+template <int KIND>
 int dispatch_gemm(int dtype, const GemmArgs& g, int R, hipStream_t s, const char* name) {
-  using KT = KindTraits<KIND>;
-  if (dtype == kBF16) {
-    const bool k_ok = KT::WGRAD || g.Kdim % pipe::BK == 0;
-    if (k_ok && g.Ndim % 8 == 0 && g.Mdim % 8 == 0) return launch_pipe<KIND>(g, R, s, name);
-    return launch_gemm<uint16_t, KIND>(g, R, s, name);
-  }
+  if (pipe_ok<KIND>(dtype, g)) return launch_pipe<KIND>(g, R, s, name);
+  if (dtype == kBF16) return launch_gemm<uint16_t, KIND>(g, R, s, name);
   return launch_gemm<float, KIND>(g, R, s, name);
+}
+
+// A data gradient and a weight gradient that share no output: one pipelined
+// launch when both kinds qualify, else one launch each.  With no routed rows
+// the data gradient is empty and the weight gradient still writes its zeros.
+template <int KD, int KW>
+int dispatch_pair(int dtype, const GemmArgs& gd, const GemmArgs& gw, int R, hipStream_t s, const char* name_d,
+                  const char* name_w, const char* name) {
+  if (R == 0) return dispatch_gemm<KW>(dtype, gw, R, s, name_w);
+  if (pipe_ok<KD>(dtype, gd) && pipe_ok<KW>(dtype, gw)) return launch_pipe_pair<KD, KW>(gd, R, gw, R, s, name);
+  if (dispatch_gemm<KD>(dtype, gd, R, s, name_d)) return 1;
+  return dispatch_gemm<KW>(dtype, gw, R, s, name_w);
 }
 
 }  // namespace abacus
@@ -1017,6 +1089,91 @@ int check_gemm_shape(int64_t R, int64_t D, int64_t M, int64_t E, int dtype) {
   ABACUS_CHECK_ARG(M >= 1 && M % vec == 0 && M < (1ll << 31), "hidden_dim %lld must be a positive multiple of %d",
                    (long long)M, vec);
   return 0;
+}
+
+// dH = dY . Wd[e]^T with the SwiGLU backward fused: B(k=d, j=m) = Wd[e][m][d],
+// k-contiguous rows of length D.
+GemmArgs args_down_dgrad(const void* dy_RD, const void* w_down_EMD, const void* gate_RM, const void* up_RM,
+                         const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E, void* dgate_RM,
+                         void* dup_RM) {
+  GemmArgs g{};
+  g.a0 = dy_RD;
+  g.b0 = w_down_EMD;
+  g.lda = D;
+  g.ldb = D;
+  g.b_estride = M * D;
+  g.c0 = dgate_RM;
+  g.c1 = dup_RM;
+  g.x0 = gate_RM;
+  g.x1 = up_RM;
+  g.ldc = M;
+  g.offsets = offsets_E1;
+  g.E = (int)E;
+  g.Mdim = (int)R;
+  g.Ndim = (int)M;
+  g.Kdim = (int)D;
+  return g;
+}
+
+// dWd[e] = H_e^T . dY_e: A(i=m, k=s) = H[s][m], B(k=s, j=d) = dY[s][d].
+GemmArgs args_down_wgrad(const void* h_RM, const void* dy_RD, const int32_t* offsets_E1, int64_t M, int64_t D,
+                         int64_t E, void* dw_down_EMD) {
+  GemmArgs g{};
+  g.a0 = h_RM;
+  g.b0 = dy_RD;
+  g.lda = M;
+  g.ldb = D;
+  g.c0 = dw_down_EMD;
+  g.ldc = D;
+  g.c_estride = M * D;
+  g.offsets = offsets_E1;
+  g.E = (int)E;
+  g.Mdim = (int)M;
+  g.Ndim = (int)D;
+  return g;
+}
+
+// dXp = dG . Wg[e]^T + dU . Wu[e]^T over the concatenated reduction:
+// B(k=m, j=d) = Wg[e][d][m], k-contiguous rows of length M.
+GemmArgs args_gateup_dgrad(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM, const void* w_up_EDM,
+                           const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, void* dx_perm_RD) {
+  GemmArgs g{};
+  g.a0 = dgate_RM;
+  g.a1 = dup_RM;
+  g.b0 = w_gate_EDM;
+  g.b1 = w_up_EDM;
+  g.lda = M;
+  g.ldb = M;
+  g.b_estride = D * M;
+  g.c0 = dx_perm_RD;
+  g.ldc = D;
+  g.offsets = offsets_E1;
+  g.E = (int)E;
+  g.Mdim = (int)R;
+  g.Ndim = (int)D;
+  g.Kdim = (int)M;
+  return g;
+}
+
+// dWg[e] = Xp_e^T . dG_e and dWu[e] = Xp_e^T . dU_e: A(i=d, k=s) = Xp[s][d],
+// B(k=s, j=m) = dG[s][m] (gate half) / dU[s][m] (up half).
+GemmArgs args_gateup_wgrad(const void* x_perm_RD, const void* dgate_RM, const void* dup_RM, const int32_t* offsets_E1,
+                           int64_t D, int64_t M, int64_t E, void* dw_gate_EDM, void* dw_up_EDM) {
+  GemmArgs g{};
+  g.a0 = x_perm_RD;
+  g.b0 = dgate_RM;
+  g.b1 = dup_RM;
+  g.lda = D;
+  g.ldb = M;
+  g.c0 = dw_gate_EDM;
+  g.c1 = dw_up_EDM;
+  g.ldc = M;
+  g.c_estride = D * M;
+  g.offsets = offsets_E1;
+  g.E = (int)E;
+  g.Mdim = (int)D;
+  g.Ndim = (int)M;
+  return g;
 }
 }  // namespace
 
@@ -1071,41 +1228,25 @@ int abacus_moe_down_bwd_dgrad(const void* dy_RD, const void* w_down_EMD, const v
                               void* dgate_RM, void* dup_RM, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   if (R == 0) return 0;
-  GemmArgs g{};
-  g.a0 = dy_RD;
-  g.b0 = w_down_EMD;   // B(k=d, j=m) = Wd[e][m][d]: k-contiguous rows of length D
-  g.lda = D;
-  g.ldb = D;
-  g.b_estride = M * D;
-  g.c0 = dgate_RM;
-  g.c1 = dup_RM;
-  g.x0 = gate_RM;
-  g.x1 = up_RM;
-  g.ldc = M;
-  g.offsets = offsets_E1;
-  g.E = (int)E;
-  g.Mdim = (int)R;
-  g.Ndim = (int)M;
-  g.Kdim = (int)D;
+  const GemmArgs g = args_down_dgrad(dy_RD, w_down_EMD, gate_RM, up_RM, offsets_E1, R, M, D, E, dgate_RM, dup_RM);
   return dispatch_gemm<kDownDgrad>(dtype, g, (int)R, (hipStream_t)stream, "down_bwd_dgrad");
 }
 
 int abacus_moe_down_bwd_wgrad(const void* h_RM, const void* dy_RD, const int32_t* offsets_E1, int64_t R, int64_t M,
                               int64_t D, int64_t E, int dtype, void* dw_down_EMD, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
-  GemmArgs g{};
-  g.a0 = h_RM;    // A(i=m, k=s) = H[s][m]
-  g.b0 = dy_RD;   // B(k=s, j=d) = dY[s][d]
-  g.lda = M;
-  g.ldb = D;
-  g.c0 = dw_down_EMD;
-  g.ldc = D;
-  g.c_estride = M * D;
-  g.offsets = offsets_E1;
-  g.E = (int)E;
-  g.Mdim = (int)M;
-  g.Ndim = (int)D;
+  const GemmArgs g = args_down_wgrad(h_RM, dy_RD, offsets_E1, M, D, E, dw_down_EMD);
   return dispatch_gemm<kDownWgrad>(dtype, g, (int)R, (hipStream_t)stream, "down_bwd_wgrad");
+}
+
+int abacus_moe_down_bwd(const void* dy_RD, const void* w_down_EMD, const void* gate_RM, const void* up_RM,
+                        const void* h_RM, const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E,
+                        int dtype, void* dgate_RM, void* dup_RM, void* dw_down_EMD, void* stream) {
+  if (check_gemm_shape(R, D, M, E, dtype)) return 1;
+  const GemmArgs gd = args_down_dgrad(dy_RD, w_down_EMD, gate_RM, up_RM, offsets_E1, R, M, D, E, dgate_RM, dup_RM);
+  const GemmArgs gw = args_down_wgrad(h_RM, dy_RD, offsets_E1, M, D, E, dw_down_EMD);
+  return dispatch_pair<kDownDgrad, kDownWgrad>(dtype, gd, gw, (int)R, (hipStream_t)stream, "down_bwd_dgrad",
+                                               "down_bwd_wgrad", "down_bwd");
 }
 
 int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM,
@@ -1113,21 +1254,7 @@ int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const 
                                 int64_t E, int dtype, void* dx_perm_RD, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   if (R == 0) return 0;
-  GemmArgs g{};
-  g.a0 = dgate_RM;
-  g.a1 = dup_RM;
-  g.b0 = w_gate_EDM;   // B(k=m, j=d) = Wg[e][d][m]: k-contiguous rows of length M
-  g.b1 = w_up_EDM;
-  g.lda = M;
-  g.ldb = M;
-  g.b_estride = D * M;
-  g.c0 = dx_perm_RD;
-  g.ldc = D;
-  g.offsets = offsets_E1;
-  g.E = (int)E;
-  g.Mdim = (int)R;
-  g.Ndim = (int)D;
-  g.Kdim = (int)M;
+  const GemmArgs g = args_gateup_dgrad(dgate_RM, dup_RM, w_gate_EDM, w_up_EDM, offsets_E1, R, D, M, E, dx_perm_RD);
   return dispatch_gemm<kGateUpDgrad>(dtype, g, (int)R, (hipStream_t)stream, "gateup_bwd_dgrad");
 }
 
@@ -1135,21 +1262,18 @@ int abacus_moe_gateup_bwd_wgrad(const void* x_perm_RD, const void* dgate_RM, con
                                 const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
                                 void* dw_gate_EDM, void* dw_up_EDM, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
-  GemmArgs g{};
-  g.a0 = x_perm_RD;   // A(i=d, k=s) = Xp[s][d]
-  g.b0 = dgate_RM;    // B(k=s, j=m) = dG[s][m]
-  g.b1 = dup_RM;
-  g.lda = D;
-  g.ldb = M;
-  g.c0 = dw_gate_EDM;
-  g.c1 = dw_up_EDM;
-  g.ldc = M;
-  g.c_estride = D * M;
-  g.offsets = offsets_E1;
-  g.E = (int)E;
-  g.Mdim = (int)D;
-  g.Ndim = (int)M;
+  const GemmArgs g = args_gateup_wgrad(x_perm_RD, dgate_RM, dup_RM, offsets_E1, D, M, E, dw_gate_EDM, dw_up_EDM);
   return dispatch_gemm<kGateUpWgrad>(dtype, g, (int)R, (hipStream_t)stream, "gateup_bwd_wgrad");
+}
+
+int abacus_moe_gateup_bwd(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM, const void* w_up_EDM,
+                          const void* x_perm_RD, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
+                          int64_t E, int dtype, void* dx_perm_RD, void* dw_gate_EDM, void* dw_up_EDM, void* stream) {
+  if (check_gemm_shape(R, D, M, E, dtype)) return 1;
+  const GemmArgs gd = args_gateup_dgrad(dgate_RM, dup_RM, w_gate_EDM, w_up_EDM, offsets_E1, R, D, M, E, dx_perm_RD);
+  const GemmArgs gw = args_gateup_wgrad(x_perm_RD, dgate_RM, dup_RM, offsets_E1, D, M, E, dw_gate_EDM, dw_up_EDM);
+  return dispatch_pair<kGateUpDgrad, kGateUpWgrad>(dtype, gd, gw, (int)R, (hipStream_t)stream, "gateup_bwd_dgrad",
+                                                   "gateup_bwd_wgrad", "gateup_bwd");
 }
 
 }  // extern "C"

@@ -192,27 +192,38 @@ class _MoEFunction(torch.autograd.Function):
             "abacus_moe_combine_bwd", ptr(dout), ptr(y), ptr(weights), ptr(score), ptr(pos), T, D, K,
             ctx.route_scale, dt, ptr(dy), ptr(dlogit), s,
         )
+        # Each data gradient and the weight gradient beside it go in one launch
+        # when both are wanted (abacus_moe_down_bwd / abacus_moe_gateup_bwd).
         dgate = torch.empty(R, M, dtype=x_TD.dtype, device=dev)
         dup = torch.empty(R, M, dtype=x_TD.dtype, device=dev)
-        call(
-            "abacus_moe_down_bwd_dgrad", ptr(dy), ptr(w_down), ptr(gate), ptr(up), ptr(offsets), R, M, D, E, dt,
-            ptr(dgate), ptr(dup), s,
-        )
         dw_down = None
         if needs[4]:
             dw_down = torch.empty_like(w_down)
-            call("abacus_moe_down_bwd_wgrad", ptr(h), ptr(dy), ptr(offsets), R, M, D, E, dt, ptr(dw_down), s)
-        dxp = None
-        if needs[0]:
-            dxp = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
             call(
-                "abacus_moe_gateup_bwd_dgrad", ptr(dgate), ptr(dup), ptr(w_gate), ptr(w_up), ptr(offsets),
-                R, D, M, E, dt, ptr(dxp), s,
+                "abacus_moe_down_bwd", ptr(dy), ptr(w_down), ptr(gate), ptr(up), ptr(h), ptr(offsets), R, M, D, E,
+                dt, ptr(dgate), ptr(dup), ptr(dw_down), s,
             )
+        else:
+            call(
+                "abacus_moe_down_bwd_dgrad", ptr(dy), ptr(w_down), ptr(gate), ptr(up), ptr(offsets), R, M, D, E, dt,
+                ptr(dgate), ptr(dup), s,
+            )
+        dxp = torch.empty(R, D, dtype=x_TD.dtype, device=dev) if needs[0] else None
         dw_gate = dw_up = None
         if needs[2] or needs[3]:
             dw_gate = torch.empty_like(w_gate)
             dw_up = torch.empty_like(w_up)
+        if dxp is not None and dw_gate is not None:
+            call(
+                "abacus_moe_gateup_bwd", ptr(dgate), ptr(dup), ptr(w_gate), ptr(w_up), ptr(xp), ptr(offsets),
+                R, D, M, E, dt, ptr(dxp), ptr(dw_gate), ptr(dw_up), s,
+            )
+        elif dxp is not None:
+            call(
+                "abacus_moe_gateup_bwd_dgrad", ptr(dgate), ptr(dup), ptr(w_gate), ptr(w_up), ptr(offsets),
+                R, D, M, E, dt, ptr(dxp), s,
+            )
+        elif dw_gate is not None:
             call(
                 "abacus_moe_gateup_bwd_wgrad", ptr(xp), ptr(dgate), ptr(dup), ptr(offsets), R, D, M, E, dt,
                 ptr(dw_gate), ptr(dw_up), s,

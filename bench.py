@@ -37,8 +37,10 @@ GEMM_FLOPS = {  # multiples of R*D*M per entry point
     "abacus_moe_down_fwd": 2,
     "abacus_moe_down_bwd_dgrad": 2,
     "abacus_moe_down_bwd_wgrad": 2,
+    "abacus_moe_down_bwd": 4,            # dgrad + wgrad in one launch
     "abacus_moe_gateup_bwd_dgrad": 4,
     "abacus_moe_gateup_bwd_wgrad": 4,
+    "abacus_moe_gateup_bwd": 8,          # dgrad + wgrad in one launch
 }
 
 

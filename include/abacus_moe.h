@@ -106,6 +106,14 @@ int abacus_moe_down_bwd_dgrad(const void* dy_RD, const void* w_down_EMD, const v
 int abacus_moe_down_bwd_wgrad(const void* h_RM, const void* dy_RD, const int32_t* offsets_E1, int64_t R, int64_t M,
                               int64_t D, int64_t E, int dtype, void* dw_down_EMD, void* stream);
 
+/* Backward of moe.py:80, both halves in one launch: abacus_moe_down_bwd_dgrad
+ * and abacus_moe_down_bwd_wgrad on the same operands (the weight gradient's
+ * short per-expert tiles fill the CUs the data gradient's last round leaves
+ * idle).  Outputs are those two calls' outputs, bit for bit. */
+int abacus_moe_down_bwd(const void* dy_RD, const void* w_down_EMD, const void* gate_RM, const void* up_RM,
+                        const void* h_RM, const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E,
+                        int dtype, void* dgate_RM, void* dup_RM, void* dw_down_EMD, void* stream);
+
 /* Backward of moe.py:78-79 (dgrad): dx_perm = dgate @ w_gate[e]^T + dup @ w_up[e]^T. */
 int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM,
                                 const void* w_up_EDM, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
@@ -115,6 +123,13 @@ int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const 
 int abacus_moe_gateup_bwd_wgrad(const void* x_perm_RD, const void* dgate_RM, const void* dup_RM,
                                 const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
                                 void* dw_gate_EDM, void* dw_up_EDM, void* stream);
+
+/* Backward of moe.py:78-79, both halves in one launch: abacus_moe_gateup_bwd_dgrad
+ * and abacus_moe_gateup_bwd_wgrad on the same operands.  Outputs are those two
+ * calls' outputs, bit for bit. */
+int abacus_moe_gateup_bwd(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM, const void* w_up_EDM,
+                          const void* x_perm_RD, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
+                          int64_t E, int dtype, void* dx_perm_RD, void* dw_gate_EDM, void* dw_up_EDM, void* stream);
 
 /* Backward of the gather of moe.py:77 plus the router GEMM of router.py:45
  * (dgrad): dx[t] = sum_k dx_perm[pos(t,k)] + sum_k dlogit(t,k) w_DE[:, e(t,k)].

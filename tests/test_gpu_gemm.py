@@ -1,0 +1,129 @@
+"""The combined backward GEMM entry points against the separate ones.
+
+abacus_moe_down_bwd and abacus_moe_gateup_bwd run a data gradient and a weight
+gradient in one launch (bf16) or as two launches (fp32, or shapes the pipelined
+kernel does not take).  Either way their outputs must equal, bit for bit, what
+the two single entry points produce on the same operands -- including experts
+with no rows and a batch with no routed rows at all (the weight gradients are
+then zeros and the data gradients empty).
+"""
+
+import itertools
+
+import pytest
+import torch
+
+from abacus_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+call, ptr = _lib.call, _lib.ptr
+
+
+def _operands(counts, D, M, dtype, seed):
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    E, R = len(counts), sum(counts)
+    offsets = torch.tensor([0] + list(itertools.accumulate(counts)), dtype=torch.int32, device=dev)
+
+    def rn(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(dtype)
+
+    return dict(
+        E=E, R=R, offsets=offsets,
+        dy=rn(R, D), w_down=rn(E, M, D, scale=0.05), gate=rn(R, M), up=rn(R, M), h=rn(R, M),
+        dgate=rn(R, M), dup=rn(R, M), w_gate=rn(E, D, M, scale=0.05), w_up=rn(E, D, M, scale=0.05), xp=rn(R, D),
+    )
+
+
+CASES = [
+    # (counts per expert, D, M): bf16 takes the single pair launch, fp32 two launches
+    ([300, 0, 500, 224], 256, 512),
+    ([0, 0, 0, 0], 256, 512),
+    ([1, 63, 0, 8], 128, 256),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("counts,D,M", CASES, ids=["ragged", "no_rows", "tiny"])
+def test_down_bwd_pair_equals_separate_calls(dtype, counts, D, M):
+    o = _operands(counts, D, M, dtype, seed=11)
+    E, R, dt = o["E"], o["R"], _lib.dtype_code(dtype)
+    s = _lib.stream_of(torch.device("cuda"))
+    out = {}
+    for mode in ("pair", "single"):
+        dg = torch.full((R, M), float("nan"), dtype=dtype, device="cuda")
+        du = torch.full((R, M), float("nan"), dtype=dtype, device="cuda")
+        dwd = torch.full((E, M, D), float("nan"), dtype=dtype, device="cuda")
+        if mode == "pair":
+            call("abacus_moe_down_bwd", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]), ptr(o["h"]),
+                 ptr(o["offsets"]), R, M, D, E, dt, ptr(dg), ptr(du), ptr(dwd), s)
+        else:
+            call("abacus_moe_down_bwd_dgrad", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]),
+                 ptr(o["offsets"]), R, M, D, E, dt, ptr(dg), ptr(du), s)
+            call("abacus_moe_down_bwd_wgrad", ptr(o["h"]), ptr(o["dy"]), ptr(o["offsets"]), R, M, D, E, dt,
+                 ptr(dwd), s)
+        out[mode] = (dg, du, dwd)
+    torch.cuda.synchronize()
+    for a, b, name in zip(out["pair"], out["single"], ("dgate", "dup", "dw_down")):
+        assert torch.equal(a, b), name
+        assert not torch.isnan(a).any(), f"{name}: unwritten elements"
+    # experts without rows get exactly zero weight gradient
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert torch.count_nonzero(out["pair"][2][e]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+@pytest.mark.parametrize("counts,D,M", CASES, ids=["ragged", "no_rows", "tiny"])
+def test_gateup_bwd_pair_equals_separate_calls(dtype, counts, D, M):
+    o = _operands(counts, D, M, dtype, seed=12)
+    E, R, dt = o["E"], o["R"], _lib.dtype_code(dtype)
+    s = _lib.stream_of(torch.device("cuda"))
+    out = {}
+    for mode in ("pair", "single"):
+        dx = torch.full((R, D), float("nan"), dtype=dtype, device="cuda")
+        dwg = torch.full((E, D, M), float("nan"), dtype=dtype, device="cuda")
+        dwu = torch.full((E, D, M), float("nan"), dtype=dtype, device="cuda")
+        if mode == "pair":
+            call("abacus_moe_gateup_bwd", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]),
+                 ptr(o["xp"]), ptr(o["offsets"]), R, D, M, E, dt, ptr(dx), ptr(dwg), ptr(dwu), s)
+        else:
+            call("abacus_moe_gateup_bwd_dgrad", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]),
+                 ptr(o["offsets"]), R, D, M, E, dt, ptr(dx), s)
+            call("abacus_moe_gateup_bwd_wgrad", ptr(o["xp"]), ptr(o["dgate"]), ptr(o["dup"]), ptr(o["offsets"]),
+                 R, D, M, E, dt, ptr(dwg), ptr(dwu), s)
+        out[mode] = (dx, dwg, dwu)
+    torch.cuda.synchronize()
+    for a, b, name in zip(out["pair"], out["single"], ("dx_perm", "dw_gate", "dw_up")):
+        assert torch.equal(a, b), name
+        assert not torch.isnan(a).any(), f"{name}: unwritten elements"
+    for e, c in enumerate(counts):
+        if c == 0:
+            assert torch.count_nonzero(out["pair"][1][e]) == 0
+            assert torch.count_nonzero(out["pair"][2][e]) == 0
+
+
+def test_pair_results_match_fp64_products():
+    """The pair launch's outputs are the products they claim to be (bf16 operands, fp64 truth)."""
+    counts, D, M = [300, 0, 500, 224], 256, 512
+    o = _operands(counts, D, M, torch.bfloat16, seed=13)
+    E, R = o["E"], o["R"]
+    s = _lib.stream_of(torch.device("cuda"))
+    dx = torch.empty(R, D, dtype=torch.bfloat16, device="cuda")
+    dwg = torch.empty(E, D, M, dtype=torch.bfloat16, device="cuda")
+    dwu = torch.empty(E, D, M, dtype=torch.bfloat16, device="cuda")
+    call("abacus_moe_gateup_bwd", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["xp"]),
+         ptr(o["offsets"]), R, D, M, E, 1, ptr(dx), ptr(dwg), ptr(dwu), s)
+    torch.cuda.synchronize()
+    off = o["offsets"].tolist()
+    f = lambda t: t.double().cpu()
+    for e in range(E):
+        a, b = off[e], off[e + 1]
+        want_dx = f(o["dgate"][a:b]) @ f(o["w_gate"][e]).T + f(o["dup"][a:b]) @ f(o["w_up"][e]).T
+        want_dwg = f(o["xp"][a:b]).T @ f(o["dgate"][a:b])
+        for got, want, name in ((dx[a:b], want_dx, "dx"), (dwg[e], want_dwg, "dw_gate")):
+            if want.numel() == 0:
+                continue
+            err = (f(got) - want).norm() / max(want.norm().item(), 1e-30)
+            assert err < 1e-2, f"expert {e} {name}: relative error {err:.3g}"
