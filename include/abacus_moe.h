@@ -43,6 +43,8 @@ int64_t abacus_moe_hist_len(int64_t T, int64_t E);
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
 /* bytes of the fp32 partial-sum scratch used by router_wgrad. */
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E);
+/* bytes of the per-block partial sums and counts used by load_balancing_fwd. */
+int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E);
 
 /* ---- forward ------------------------------------------------------------ */
 
@@ -150,6 +152,26 @@ int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, co
 /* Router.update_bias (router.py:57-70) for an explicit int64 index tensor. */
 int abacus_router_update_bias(const int64_t* indices_i64, int64_t N, int64_t E, float speed, int dtype,
                               void* bias_E, void* stream);
+
+/* ---- auxiliary loss -------------------------------------------------------- */
+
+/* load_balancing.py:30-41 (Switch-Transformer auxiliary loss) on (T, E) router
+ * probabilities and (T, K) int64 expert slots: f_E = distinct-expert count per
+ * token / (T*K) (one_hot(...).amax(1), :36-38), p_E = column mean in fp32 (:39),
+ * loss = sum(f_E * p_E) * coeff_e (:40) with coeff_e = coeff * E as fp32,
+ * written as fp32 and in `dtype` (:41).  f_E (E fp32) is kept for the backward.
+ * Slots outside [0, E) set bad_index (bit 0: negative, bit 1: >= E) for the
+ * caller to raise on, as torch.nn.functional.one_hot does; T must be > 0 (the
+ * reference returns a zero without computing anything).  Deterministic. */
+int abacus_moe_load_balancing_fwd(const void* probs_TE, const int64_t* slots_TK, int64_t T, int64_t E, int64_t K,
+                                  float coeff_e, int dtype, void* ws, float* f_E, float* loss_f32, void* loss_out,
+                                  int32_t* bad_index, void* stream);
+
+/* Autograd of the above with respect to the probabilities: grad_probs[t, e] =
+ * ((g * coeff_e) * f_E[e]) / T in fp32, rounded to `dtype`, g = the loss
+ * gradient (one `dtype` element on the device). */
+int abacus_moe_load_balancing_bwd(const void* grad_loss, const float* f_E, int64_t T, int64_t E, float coeff_e,
+                                  int dtype, void* grad_probs_TE, void* stream);
 
 #ifdef __cplusplus
 }

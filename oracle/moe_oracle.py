@@ -7,6 +7,7 @@ part of the product path.
 It restates, in this project's own code, the algorithm of
   abacus/moe/router.py:40-70   (sigmoid router, selection bias, top-k, renormalise, bias step)
   abacus/moe/moe.py:60-86      (per-expert mask -> gather -> SwiGLU -> weighted scatter -> stack-sum)
+  abacus/moe/load_balancing.py:8-41 (Switch-Transformer auxiliary loss)
 with the same per-op rounding as torch on CPU in the activation dtype.
 
 Pinning (tests/test_oracle.py):
@@ -20,6 +21,9 @@ Pinning (tests/test_oracle.py):
                           forced routing (w_DE = +-8) equals expert 0's MLP
   moe backward          - fp64 torch.autograd.gradcheck; closed_form_backward (Appendix-A
                           formulas in numpy fp64) against autograd
+  load_balancing_loss   - closed forms (uniform routing -> coeff; collapsed routing ->
+                          coeff * E); Python-loop brute force in fp64 with repeated slots;
+                          gradient = coeff * E * f_E / T per element against autograd
 Parity pinned this way for every function above; nothing is left "unpinned".
 
 Tie rule (the reference leaves it to torch.topk, whose order among equal values
@@ -260,3 +264,64 @@ def sigmoid_reference_scalar(v: float) -> float:
         return 1.0 / (1.0 + math.exp(-v))
     z = math.exp(v)
     return z / (1.0 + z)
+
+
+# ---------------------------------------------------------------------------
+# Switch-Transformer auxiliary loss (load_balancing.py:8-41)
+# ---------------------------------------------------------------------------
+def load_balancing_loss(router_probs: torch.Tensor, expert_indices: torch.Tensor, coeff: float = 1e-2):
+    """Restatement of load_balancing.py:8-41 on CPU tensors; differentiable in router_probs.
+
+    f_E: fraction of (token, slot) pairs per expert with each expert counted at
+    most once per token (the reference's one_hot(...).amax(dim=1), here a scatter
+    of ones); p_E: mean probability per expert in fp32; loss = sum(f_E * p_E) *
+    (coeff * E), returned in router_probs' dtype.
+    """
+    if router_probs.ndim < 1:  # load_balancing.py:14-15
+        raise ValueError("router_probs must include an expert dimension")
+    n_experts = router_probs.shape[-1]
+    if n_experts < 1:  # :17-18
+        raise ValueError(f"router_probs has no experts, got shape {tuple(router_probs.shape)}")
+    batch = router_probs.shape[:-1]
+    if expert_indices.shape[: len(batch)] != batch:  # :20-24
+        raise ValueError(
+            f"expert_indices shape {tuple(expert_indices.shape)} does not match "
+            f"router_probs batch {tuple(batch)}"
+        )
+    extra = expert_indices.ndim - len(batch)
+    if extra > 1:  # :26-29
+        raise ValueError(f"expert_indices has {extra} expert-choice dimensions, expected 0 or 1")
+    probs_TE = router_probs.reshape(-1, n_experts).float()  # :30
+    tokens = probs_TE.shape[0]
+    if tokens == 0:  # :32-33
+        return router_probs.new_zeros(())
+    slots_TK = expert_indices.reshape(tokens, -1).to(dtype=torch.long)  # :34
+    # torch.nn.functional.one_hot's own argument checks (:36)
+    if slots_TK.numel() > 0:
+        if int(slots_TK.min()) < 0:
+            raise RuntimeError("Class values must be non-negative.")
+        if int(slots_TK.max()) >= n_experts:
+            raise RuntimeError("Class values must be smaller than num_classes.")
+    k = slots_TK.shape[-1]
+    if k == 0:  # amax over an empty slot dimension
+        raise RuntimeError("amax(): Expected reduction dim 1 to have non-zero size.")
+    dispatch_TE = torch.zeros(tokens, n_experts, dtype=torch.float32).scatter_(1, slots_TK, 1.0)  # :36
+    f_E = dispatch_TE.sum(dim=0) / (tokens * k)  # :38
+    p_E = probs_TE.sum(dim=0) / tokens  # :39
+    loss = torch.sum(f_E * p_E) * (coeff * n_experts)  # :40
+    return loss.to(dtype=router_probs.dtype)  # :41
+
+
+def load_balancing_bruteforce(probs, indices, coeff):
+    """Python-loop restatement in fp64 (tiny inputs): the definition read off load_balancing.py:36-40."""
+    P = [[float(v) for v in row] for row in probs.reshape(-1, probs.shape[-1]).tolist()]
+    T, E = len(P), probs.shape[-1]
+    S = indices.reshape(T, -1).tolist()
+    K = len(S[0])
+    f = [0.0] * E
+    for t in range(T):
+        for e in set(S[t]):
+            f[e] += 1.0
+    f = [c / (T * K) for c in f]
+    p = [sum(P[t][e] for t in range(T)) / T for e in range(E)]
+    return sum(f[e] * p[e] for e in range(E)) * coeff * E

@@ -1,6 +1,7 @@
 """Host-side API of the drop-in modules (no GPU compute): constructors, parameter layout,
-initialisation RNG order and error behaviour of abacus.moe.{moe,router} (reference:
-abacus/moe/router.py:15-37, abacus/moe/moe.py:25-57, :92-128)."""
+initialisation RNG order and error behaviour of abacus.moe.{moe,router,load_balancing}
+(reference: abacus/moe/router.py:15-37, abacus/moe/moe.py:25-57, :92-128,
+abacus/moe/load_balancing.py:14-33)."""
 
 import pytest
 import torch
@@ -8,6 +9,7 @@ import torch
 from abacus.mlp import MLP
 from abacus.moe.moe import MoE, MoEExpertParallel
 from abacus.moe.router import Router
+from oracle import moe_oracle as oracle
 
 
 def test_parameter_layout_and_state_dict():
@@ -95,3 +97,31 @@ def test_dense_mlp_matches_linear_layers():
         up.weight.copy_(mlp.w_up_DM.T)
         down.weight.copy_(mlp.w_down_MD.T)
     torch.testing.assert_close(mlp(x), down(torch.nn.functional.silu(gate(x)) * up(x)))
+
+
+# ---------------------------------------------------------------------------
+# load_balancing_loss (load_balancing.py:8-41): the checks that run before any
+# kernel, against the oracle's restatement of the reference
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("probs,idx", [
+    (torch.tensor(1.0), torch.tensor(0)),
+    (torch.zeros(3, 0), torch.zeros(3, 1, dtype=torch.long)),
+    (torch.zeros(3, 4), torch.zeros(2, 1, dtype=torch.long)),
+    (torch.zeros(3, 4), torch.zeros(3, 1, 1, dtype=torch.long)),
+    (torch.zeros(2, 3, 4), torch.zeros(3, 2, dtype=torch.long)),
+])
+def test_load_balancing_value_errors_match_reference(probs, idx):
+    from abacus.moe.load_balancing import load_balancing_loss
+    with pytest.raises(ValueError) as want:
+        oracle.load_balancing_loss(probs, idx)
+    with pytest.raises(ValueError) as got:
+        load_balancing_loss(probs, idx)
+    assert str(got.value) == str(want.value)
+
+
+def test_load_balancing_empty_and_cpu():
+    from abacus.moe.load_balancing import load_balancing_loss
+    z = load_balancing_loss(torch.zeros(0, 5, dtype=torch.bfloat16), torch.zeros(0, 2, dtype=torch.long))
+    assert z.shape == () and z.dtype == torch.bfloat16 and float(z) == 0.0
+    with pytest.raises(RuntimeError, match="ROCm"):
+        load_balancing_loss(torch.rand(4, 3), torch.zeros(4, 1, dtype=torch.long))

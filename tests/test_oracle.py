@@ -10,6 +10,7 @@ import math
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import moe_oracle as oracle
 
@@ -185,3 +186,85 @@ def test_empty_tokens_returns_input():
     out, _ = oracle.moe_forward(x, torch.zeros(4, 2), torch.zeros(2), torch.zeros(2, 4, 3), torch.zeros(2, 4, 3),
                                 torch.zeros(2, 3, 4), top_k=1)
     assert out is x
+
+
+# ---------------------------------------------------------------------------
+# load_balancing.py:8-41
+# ---------------------------------------------------------------------------
+def test_load_balancing_uniform_routing_is_coeff():
+    # every expert gets 1/E of the slots and 1/E of the probability: sum(f p) = 1/E, times coeff * E
+    E = 8
+    probs = torch.full((E * 3, E), 1.0 / E)
+    idx = torch.arange(E * 3).remainder(E).unsqueeze(1)
+    loss = oracle.load_balancing_loss(probs, idx, coeff=0.03)
+    assert abs(float(loss) - 0.03) < 1e-7
+
+
+def test_load_balancing_collapsed_routing_is_coeff_times_e():
+    E = 6
+    probs = torch.zeros(10, E)
+    probs[:, 0] = 1.0
+    idx = torch.zeros(10, 2, dtype=torch.long)  # both slots repeat expert 0: counted once per token
+    loss = oracle.load_balancing_loss(probs, idx, coeff=0.01)
+    # f_0 = 10 / (10 * 2) = 0.5 (one count per token, K = 2), p_0 = 1
+    assert abs(float(loss) - 0.5 * 1.0 * 0.01 * E) < 1e-7
+
+
+@pytest.mark.parametrize("T,E,K,seed", [(1, 1, 1, 0), (5, 4, 3, 1), (17, 8, 2, 2), (9, 5, 6, 3)])
+def test_load_balancing_matches_bruteforce(T, E, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    probs = torch.rand(T, E, generator=g, dtype=torch.float64)
+    idx = torch.randint(0, E, (T, K), generator=g)  # repeats within a token are likely
+    got = oracle.load_balancing_loss(probs.float(), idx, coeff=0.02)
+    want = oracle.load_balancing_bruteforce(probs.float(), idx, 0.02)
+    assert abs(float(got) - want) <= 1e-6 * max(abs(want), 1e-6)
+
+
+def test_load_balancing_batch_dims_and_no_slot_dim():
+    g = torch.Generator().manual_seed(4)
+    probs = torch.rand(2, 3, 4, generator=g)
+    idx = torch.randint(0, 4, (2, 3), generator=g)  # no expert-choice dimension: K = 1
+    got = oracle.load_balancing_loss(probs, idx)
+    want = oracle.load_balancing_bruteforce(probs, idx.unsqueeze(-1), 1e-2)
+    assert abs(float(got) - want) <= 1e-6 * abs(want)
+
+
+def test_load_balancing_gradient_closed_form():
+    # d loss / d probs[t, e] = coeff * E * f_E[e] / T: read off load_balancing.py:38-40
+    g = torch.Generator().manual_seed(5)
+    T, E, K, coeff = 7, 5, 2, 0.04
+    probs = torch.rand(T, E, generator=g).requires_grad_()
+    idx = torch.randint(0, E, (T, K), generator=g)
+    oracle.load_balancing_loss(probs, idx, coeff).backward()
+    f = torch.zeros(E)
+    for t in range(T):
+        for e in set(idx[t].tolist()):
+            f[e] += 1.0 / (T * K)
+    want = (coeff * E * f / T).expand(T, E)
+    torch.testing.assert_close(probs.grad, want, rtol=1e-6, atol=1e-9)
+
+
+def test_load_balancing_errors_and_empty():
+    with pytest.raises(ValueError, match="must include an expert dimension"):
+        oracle.load_balancing_loss(torch.tensor(1.0), torch.tensor(0))
+    with pytest.raises(ValueError, match="has no experts"):
+        oracle.load_balancing_loss(torch.zeros(3, 0), torch.zeros(3, 1, dtype=torch.long))
+    with pytest.raises(ValueError, match="does not match"):
+        oracle.load_balancing_loss(torch.zeros(3, 4), torch.zeros(2, 1, dtype=torch.long))
+    with pytest.raises(ValueError, match="expert-choice dimensions"):
+        oracle.load_balancing_loss(torch.zeros(3, 4), torch.zeros(3, 1, 1, dtype=torch.long))
+    with pytest.raises(RuntimeError, match="non-negative"):
+        oracle.load_balancing_loss(torch.zeros(3, 4), torch.full((3, 1), -1))
+    with pytest.raises(RuntimeError, match="smaller than num_classes"):
+        oracle.load_balancing_loss(torch.zeros(3, 4), torch.full((3, 1), 4))
+    z = oracle.load_balancing_loss(torch.zeros(0, 4, dtype=torch.bfloat16), torch.zeros(0, 2, dtype=torch.long))
+    assert z.shape == () and z.dtype == torch.bfloat16 and float(z) == 0.0
+
+
+def test_load_balancing_one_hot_agrees_with_scatter():
+    # the restatement's scatter of ones equals the reference's one_hot(...).amax(dim=1)
+    g = torch.Generator().manual_seed(6)
+    idx = torch.randint(0, 7, (40, 5), generator=g)
+    want = F.one_hot(idx, 7).amax(dim=1).float()
+    got = torch.zeros(40, 7).scatter_(1, idx, 1.0)
+    assert torch.equal(got, want)
