@@ -1,0 +1,315 @@
+"""The MoE decoder that calls the MoE layer: TransformerMoe and its parts.
+
+Single-GPU restatements of the reference's caller modules, with their
+constructor signatures, parameter names and shapes, buffers and
+initialisation RNG order, so a seeded model and its state_dict match the
+reference's:
+
+  Embedding            abacus/embedding.py:8-23
+  Rotary, rotate_half,
+  apply_rotary_pos_emb abacus/rope.py:9-46
+  RMSNorm              abacus/norm.py:11-31
+  MultiHeadAttention   abacus/attention.py:67-150, 188-218 (the single-rank path)
+  TransformerBlockMoe  abacus/transformer_block.py:64-110
+  TransformerMoe       abacus/transformer_moe.py:17-75
+
+The MoE layer inside each block is abacus_amd.moe.MoE (the HIP path).  The
+rest runs on torch.  Causal attention is materialised like the reference's
+(scores, mask, softmax, weighted sum), written as one autograd function whose
+batched products all take contiguous operands.  Tensor, sequence and context
+parallelism with more than one process are not part of this build.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .moe import MoE, MoEExpertParallel, _rank_and_world_size
+
+__all__ = [
+    "Embedding",
+    "Rotary",
+    "rotate_half",
+    "apply_rotary_pos_emb",
+    "RMSNorm",
+    "MultiHeadAttention",
+    "TransformerBlockMoe",
+    "TransformerMoe",
+]
+
+
+def _single_process(what: str) -> None:
+    if _rank_and_world_size()[1] > 1:
+        raise NotImplementedError(f"{what} across processes is not part of this single-GPU build")
+
+
+class Embedding(torch.nn.Module):
+    """Token embedding table (embedding.py:8-23): w_vocab_D ~ N(0, 1)."""
+
+    def __init__(self, vocab_size: int, dim: int):
+        super().__init__()
+        self.vocab_size = vocab_size
+        self.dim = dim
+        self.w_vocab_D = torch.nn.Parameter(torch.empty(vocab_size, dim))
+        torch.nn.init.normal_(self.w_vocab_D)
+
+    def forward(self, tokens_BL: torch.Tensor) -> torch.Tensor:
+        return self.w_vocab_D[tokens_BL]  # (B, L, D)
+
+
+class Rotary(torch.nn.Module):
+    """Rotary position tables (rope.py:9-32): cos/sin of position x inv_freq, cached per length.
+
+    inv_freq is a buffer, so Module.to(dtype) casts it and the tables follow
+    the model's dtype, as in the reference.
+    """
+
+    def __init__(self, dim: int, base: float = 10000):
+        super().__init__()
+        inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2).float() / dim))  # (K / 2,)
+        self.register_buffer("inv_freq", inv_freq)
+        self.seq_len_cached = None
+        self.cos_cached = None
+        self.sin_cached = None
+
+    def forward(self, x: torch.Tensor, seq_dim: int = 2, positions: torch.Tensor | None = None):
+        if positions is not None:
+            return self._angles(x, positions)
+        seq_len = x.shape[seq_dim]
+        if seq_len != self.seq_len_cached:
+            self.seq_len_cached = seq_len
+            self.cos_cached, self.sin_cached = self._angles(x, torch.arange(seq_len, device=x.device))
+        return self.cos_cached, self.sin_cached  # (1, 1, L, K)
+
+    def _angles(self, x: torch.Tensor, positions: torch.Tensor):
+        t = positions.to(device=x.device).type_as(self.inv_freq)  # (L,)
+        freqs = torch.outer(t, self.inv_freq)  # (L, K / 2)
+        emb = torch.cat((freqs, freqs), dim=-1).to(x.device)  # (L, K)
+        return emb.cos()[None, None, :, :], emb.sin()[None, None, :, :]
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """(x1, x2) -> (-x2, x1) over the last dimension's halves (rope.py:35-40)."""
+    half = x.shape[-1] // 2
+    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+
+
+def apply_rotary_pos_emb(q, k, cos, sin):
+    """q cos + rotate_half(q) sin, likewise for k (rope.py:43-46)."""
+    return (q * cos) + (rotate_half(q) * sin), (k * cos) + (rotate_half(k) * sin)
+
+
+class RMSNorm(torch.nn.Module):
+    """gamma * x / sqrt(mean(x^2) + 1e-5) over the last dimension (norm.py:11-31)."""
+
+    def __init__(self, dim: int, sequence_parallel: bool = False, sync_grads: bool = False):
+        super().__init__()
+        self.dim = dim
+        self.sequence_parallel = sequence_parallel
+        self.sync_grads = sequence_parallel or sync_grads
+        self.world_size = _rank_and_world_size()[1] if self.sync_grads else 1
+        self.w_gamma_D = torch.nn.Parameter(torch.ones(self.dim))
+
+    def forward(self, x_BLD: torch.Tensor) -> torch.Tensor:
+        if self.sync_grads and self.world_size > 1:
+            _single_process("RMSNorm gradient synchronisation")
+        rms_BL = torch.sqrt(x_BLD.square().mean(dim=-1, keepdim=True) + 1e-5)  # (B, L, 1)
+        return self.w_gamma_D * x_BLD / rms_BL
+
+
+class _CausalAttention(torch.autograd.Function):
+    """softmax(mask(q k^T / sqrt(K))) v over (B*H, L, K) blocks (attention.py:136-141).
+
+    Forward and backward as four batched products whose operands are all
+    contiguous; the softmax backward is torch's own kernel, so the gradients
+    are the ones autograd would form from the same forward.
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale_div: float):
+        BH, L, K = q.shape
+        s = torch.bmm(q, k.transpose(1, 2).contiguous())  # (BH, L, L)
+        s = s / scale_div
+        later = torch.ones(L, L, dtype=torch.bool, device=q.device).triu_(1)  # key after its query
+        s = s.masked_fill(later, float("-inf"))
+        p = torch.softmax(s, dim=-1)
+        out = torch.bmm(p, v)  # (BH, L, K)
+        ctx.save_for_backward(q, k, v, p)
+        ctx.scale_div = scale_div
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        q, k, v, p = ctx.saved_tensors
+        d_out = d_out.contiguous()
+        d_p = torch.bmm(d_out, v.transpose(1, 2).contiguous())
+        d_v = torch.bmm(p.transpose(1, 2).contiguous(), d_out)
+        d_s = torch._softmax_backward_data(d_p, p, -1, p.dtype)  # zero where the mask put -inf
+        d_s = d_s / ctx.scale_div
+        d_q = torch.bmm(d_s, k)
+        d_k = torch.bmm(d_s.transpose(1, 2).contiguous(), q)
+        return d_q, d_k, d_v, None
+
+
+class MultiHeadAttention(torch.nn.Module):
+    """Causal multi-head attention with QK-norm and RoPE (attention.py:67-150).
+
+    Parameters w_q_DHK, w_k_DHK, w_v_DHK (D, H, K), w_o_HKD (H, K, D) drawn
+    with xavier_uniform_ on their (D, H*K) / (H*K, D) views in that order,
+    then q_norm and k_norm (RMSNorm over K).
+    """
+
+    def __init__(
+        self,
+        dim: int,
+        n_heads: int,
+        head_dim: int,
+        tensor_parallel: bool = False,
+        sequence_parallel: bool = False,
+        context_parallel: bool = False,
+    ):
+        super().__init__()
+        if sequence_parallel and not tensor_parallel:
+            raise ValueError("sequence_parallel requires tensor_parallel")
+        if context_parallel and (tensor_parallel or sequence_parallel):
+            raise ValueError("context_parallel does not combine with tensor or sequence parallel")
+        self.dim = dim
+        self.n_heads = n_heads
+        self.head_dim = head_dim
+        self.tensor_parallel = tensor_parallel
+        self.sequence_parallel = sequence_parallel
+        self.context_parallel = context_parallel
+        if tensor_parallel:
+            self.rank, self.world_size = _rank_and_world_size()
+            if n_heads % self.world_size != 0:
+                raise ValueError(f"n_heads {n_heads} is not divisible by world size {self.world_size}")
+        else:
+            self.rank, self.world_size = 0, 1
+        self.local_heads = n_heads // self.world_size
+        q_DHK = torch.empty(dim, n_heads, head_dim)
+        k_DHK = torch.empty(dim, n_heads, head_dim)
+        v_DHK = torch.empty(dim, n_heads, head_dim)
+        o_HKD = torch.empty(n_heads, head_dim, dim)
+        for w in (q_DHK, k_DHK, v_DHK):
+            torch.nn.init.xavier_uniform_(w.view(dim, n_heads * head_dim))
+        torch.nn.init.xavier_uniform_(o_HKD.view(n_heads * head_dim, dim))
+        h0, h1 = self.rank * self.local_heads, (self.rank + 1) * self.local_heads
+        self.w_q_DHK = torch.nn.Parameter(q_DHK[:, h0:h1].clone())
+        self.w_k_DHK = torch.nn.Parameter(k_DHK[:, h0:h1].clone())
+        self.w_v_DHK = torch.nn.Parameter(v_DHK[:, h0:h1].clone())
+        self.w_o_HKD = torch.nn.Parameter(o_HKD[h0:h1].clone())
+        sync_qk = tensor_parallel or context_parallel
+        self.q_norm = RMSNorm(head_dim, sync_grads=sync_qk)
+        self.k_norm = RMSNorm(head_dim, sync_grads=sync_qk)
+
+    def _split_heads(self, x_BLD: torch.Tensor, w_DHK: torch.Tensor) -> torch.Tensor:
+        B, L, _ = x_BLD.shape
+        projected = x_BLD @ w_DHK.reshape(self.dim, self.local_heads * self.head_dim)  # (B, L, H*K)
+        return projected.view(B, L, self.local_heads, self.head_dim).permute(0, 2, 1, 3)  # (B, H, L, K)
+
+    def forward(self, x_BLD: torch.Tensor, rotary: Rotary | None = None) -> torch.Tensor:
+        if self.context_parallel or self.world_size > 1:
+            _single_process("attention parallelism")
+        B, L, _ = x_BLD.shape
+        H, K = self.local_heads, self.head_dim
+        q = self.q_norm(self._split_heads(x_BLD, self.w_q_DHK))
+        k = self.k_norm(self._split_heads(x_BLD, self.w_k_DHK))
+        v = self._split_heads(x_BLD, self.w_v_DHK)
+        if rotary is not None:
+            cos, sin = rotary(q, seq_dim=2)
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        out = _CausalAttention.apply(
+            q.reshape(B * H, L, K).contiguous(), k.reshape(B * H, L, K).contiguous(),
+            v.reshape(B * H, L, K).contiguous(), self.head_dim ** 0.5,
+        )  # (B*H, L, K)
+        joined = out.view(B, H, L, K).permute(0, 2, 1, 3).reshape(B, L, H * K)
+        return joined @ self.w_o_HKD.reshape(H * K, self.dim)  # (B, L, D)
+
+
+class TransformerBlockMoe(torch.nn.Module):
+    """x + attention(RMSNorm(x)), then x + MoE(RMSNorm(x)) (transformer_block.py:64-110)."""
+
+    def __init__(
+        self,
+        dim: int,
+        n_heads: int,
+        head_dim: int,
+        n_experts: int,
+        top_k: int,
+        dropout: float = 0.0,
+        hidden_dim: int | None = None,
+        bias_update_speed: float = 1e-3,
+        route_scale: float = 1.0,
+        expert_parallel: bool = False,
+    ):
+        super().__init__()
+        _, world_size = _rank_and_world_size()
+        if expert_parallel and dropout > 0 and world_size > 1:
+            raise ValueError("expert parallel keeps dropout at 0 so replicated layers stay identical")
+        self.dim = dim
+        self.n_heads = n_heads
+        self.head_dim = head_dim
+        self.norm_attention = RMSNorm(dim)
+        self.attention = MultiHeadAttention(dim, n_heads, head_dim)
+        self.norm_mlp = RMSNorm(dim)
+        moe = MoEExpertParallel if expert_parallel else MoE
+        self.moe = moe(
+            dim, n_experts, top_k, hidden_dim=hidden_dim, bias_update_speed=bias_update_speed,
+            route_scale=route_scale,
+        )
+        self.dropout = torch.nn.Dropout(dropout)
+
+    def forward(self, x_BLD: torch.Tensor, rotary: torch.nn.Module | None = None) -> torch.Tensor:
+        attn_BLD = self.attention(self.norm_attention(x_BLD), rotary)
+        x_BLD = x_BLD + self.dropout(attn_BLD)
+        moe_BLD = self.moe(self.norm_mlp(x_BLD))
+        return x_BLD + self.dropout(moe_BLD)
+
+
+class TransformerMoe(torch.nn.Module):
+    """Embedding -> n_blocks x TransformerBlockMoe -> RMSNorm -> logits (transformer_moe.py:17-75)."""
+
+    def __init__(
+        self,
+        dim: int,
+        n_heads: int,
+        head_dim: int,
+        n_blocks: int,
+        vocab_size: int,
+        n_experts: int,
+        top_k: int,
+        dropout: float = 0.0,
+        hidden_dim: int | None = None,
+        bias_update_speed: float = 1e-3,
+        route_scale: float = 1.0,
+        expert_parallel: bool = False,
+    ):
+        super().__init__()
+        self.dim = dim
+        self.n_heads = n_heads
+        self.head_dim = head_dim
+        self.n_blocks = n_blocks
+        self.vocab_size = vocab_size
+        self.n_experts = n_experts
+        self.top_k = top_k
+        self.expert_parallel = expert_parallel
+        self.embedding = Embedding(vocab_size, dim)
+        self.rotary = Rotary(head_dim)
+        self.blocks = torch.nn.ModuleList(
+            [
+                TransformerBlockMoe(
+                    dim, n_heads, head_dim, n_experts, top_k, dropout, hidden_dim=hidden_dim,
+                    bias_update_speed=bias_update_speed, route_scale=route_scale, expert_parallel=expert_parallel,
+                )
+                for _ in range(n_blocks)
+            ]
+        )
+        self.norm = RMSNorm(dim)
+        self.w_D_vocab = torch.nn.Parameter(torch.empty(dim, vocab_size))  # (D, vocab)
+        torch.nn.init.xavier_uniform_(self.w_D_vocab)
+
+    def forward(self, tokens_BL: torch.Tensor) -> torch.Tensor:
+        x_BLD = self.embedding(tokens_BL)
+        for block in self.blocks:
+            x_BLD = block(x_BLD, self.rotary)
+        return self.norm(x_BLD) @ self.w_D_vocab  # (B, L, vocab)

@@ -49,7 +49,9 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--workload", default="mixtral_bf16")
+    p.add_argument("--workload", default="mixtral_bf16",
+                   help="an MoE-layer workload of abacus_amd.workloads, or decoder_bf16 / decoder_fp32 "
+                        "(the full MoE decoder training step)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample duration")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -147,6 +149,72 @@ def cpu_baseline(wl, target_seconds):
     }
 
 
+# The full small MoE decoder training step (transformer_moe.py architecture):
+# 8 layers, d_model 1024, 16 heads of 64 with RoPE and QK-norm, vocab 32000, an
+# MoE FFN in every layer (16 experts, top-2, SwiGLU hidden 2816); batch 4 x
+# 2048 token ids uniform in [0, 32000), seed 4; one AdamW step per step.
+DECODER = dict(dim=1024, n_heads=16, head_dim=64, n_blocks=8, vocab_size=32000, n_experts=16, top_k=2,
+               hidden_dim=2816)
+DECODER_BATCH, DECODER_SEQ, DECODER_SEED = 4, 2048, 4
+
+
+def bench_decoder(args, dtype):
+    """Training-step tokens/s of the MoE decoder and the MoE kernels' share of the step."""
+    from abacus_amd import _lib
+    from abacus_amd.train import make_optimizer, train_step
+    from abacus_amd.transformer import TransformerMoe
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    torch.manual_seed(DECODER_SEED)
+    model = TransformerMoe(**DECODER)  # built on the host: the reference constructors' RNG order
+    tokens = torch.randint(0, DECODER["vocab_size"], (DECODER_BATCH, DECODER_SEQ))
+    model = model.to(dtype).to(dev)
+    tokens = tokens.to(dev)
+    opt = make_optimizer(model)
+    for _ in range(args.warmup):
+        train_step(model, opt, tokens)
+    torch.cuda.synchronize()
+    timer = _lib.KernelTimer()
+    losses = []
+    t0 = time.perf_counter()
+    with timer:
+        for _ in range(args.steps):
+            losses.append(train_step(model, opt, tokens))
+        torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = 1000.0 * elapsed / args.steps
+    totals = timer.totals_ms()
+    moe_ms = sum(ms for ms, _ in totals.values()) / args.steps
+    kernels = {name: {"avg_us": round(ms / n * 1000.0, 2), "calls": n, "share": round(ms / (elapsed * 1000.0), 4)}
+               for name, (ms, n) in sorted(totals.items(), key=lambda kv: -kv[1][0])}
+    tok = DECODER_BATCH * DECODER_SEQ
+    n_params = sum(p.numel() for p in model.parameters())
+    return {
+        "metric": "MoE decoder training step tokens/sec on 1 MI355X (forward, cross-entropy, backward, AdamW)",
+        "value": round(tok / (ms_per_step / 1000.0), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
+        "data": f"synthetic token ids uniform in [0, {DECODER['vocab_size']}), seed {DECODER_SEED}; random init",
+        "config": {"workload": f"MoE decoder training step: {DECODER['n_blocks']} layers, d_model {DECODER['dim']}, "
+                               f"{DECODER['n_heads']} heads x {DECODER['head_dim']}, vocab {DECODER['vocab_size']}, "
+                               f"MoE E={DECODER['n_experts']} K={DECODER['top_k']} M={DECODER['hidden_dim']} in "
+                               f"every layer; batch {DECODER_BATCH} x seq {DECODER_SEQ}",
+                   "parameters": n_params, "tokens_per_step": tok},
+        "moe_share": round(moe_ms / ms_per_step, 4),
+        "moe_ms_per_step": round(moe_ms, 4),
+        "loss_first_last": [round(float(losses[0]), 4), round(float(losses[-1]), 4)],
+        "kernels": kernels,
+    }
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -156,6 +224,11 @@ def main():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from abacus_amd import _lib
     from abacus_amd import workloads as W
+
+    if args.workload in ("decoder_bf16", "decoder_fp32"):
+        dt = torch.bfloat16 if args.workload == "decoder_bf16" else torch.float32
+        print(json.dumps(bench_decoder(args, dt)), flush=True)
+        return
 
     wl = W.ALL[args.workload]
     dev = torch.device("cuda", 0)

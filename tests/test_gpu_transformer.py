@@ -1,0 +1,100 @@
+"""TransformerMoe (transformer_moe.py:17-75) on the GPU, MoE layers on the HIP path.
+
+The same seeded model runs three ways: on the GPU, on the CPU in the same dtype,
+and on the CPU in fp64 (the truth).  On the CPU each block's MoE is the oracle's
+restatement, fed the routing the GPU chose so that a near-tie top-k cannot make
+the runs diverge.  Criterion (as in test_gpu_moe.py): the GPU's normwise error
+against fp64 is within twice the CPU's, or below the dtype's rtol (fp32 1e-5,
+bf16 2e-2).
+"""
+
+import copy
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from abacus.transformer_moe import TransformerMoe
+from oracle import moe_oracle as oracle
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(dim=64, n_heads=4, head_dim=16, n_blocks=2, vocab_size=97, n_experts=4, top_k=2, hidden_dim=96)
+RTOL = {torch.float32: 1e-5, torch.bfloat16: 2e-2}
+
+
+class _OracleMoE(torch.nn.Module):
+    """CPU MoE from the oracle with fixed routing; shares the replaced module's parameters."""
+
+    def __init__(self, moe, indices_TK):
+        super().__init__()
+        self.moe, self.indices = moe, indices_TK
+
+    def forward(self, x_BLD):
+        m = self.moe
+        out, _ = oracle.moe_forward(
+            x_BLD.reshape(-1, m.dim), m.router.w_DE, m.router.expert_bias_E, m.w_gate_EDM, m.w_up_EDM, m.w_down_EMD,
+            m.top_k, m.router.route_scale, indices_TK=self.indices,
+        )
+        return out.reshape(x_BLD.shape)
+
+
+def _run(model, tokens):
+    logits = model(tokens)
+    loss = F.cross_entropy(logits[:, :-1].reshape(-1, logits.shape[-1]).float(), tokens[:, 1:].reshape(-1))
+    loss.backward()
+    # the CPU models wrap each MoE once: blocks.i.moe.moe.* names the same parameter as blocks.i.moe.*
+    grads = {n.replace(".moe.moe.", ".moe."): p.grad.detach().double().cpu()
+             for n, p in model.named_parameters() if p.grad is not None}
+    return logits.detach().double().cpu(), grads
+
+
+def _rel(a, b):
+    return float((a - b).norm() / max(b.norm().item(), 1e-30))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_transformer_moe_matches_cpu_restatement(dtype):
+    torch.manual_seed(4)
+    base = TransformerMoe(**CFG).eval()
+    tokens = torch.randint(0, CFG["vocab_size"], (2, 24))
+
+    gpu = copy.deepcopy(base).to(dtype).cuda()
+    got_logits, got_grads = _run(gpu, tokens.cuda())
+    routes = [blk.moe.router.last_routing.indices_TK.detach().long().cpu() for blk in gpu.blocks]
+
+    def cpu_model(dt):
+        m = copy.deepcopy(base).to(dt)
+        for blk, idx in zip(m.blocks, routes):
+            blk.moe = _OracleMoE(blk.moe, idx)
+        return m
+
+    ref_logits, ref_grads = _run(cpu_model(dtype), tokens)
+    tru_logits, tru_grads = _run(cpu_model(torch.float64), tokens)
+
+    rtol = RTOL[dtype]
+    e_gpu, e_cpu = _rel(got_logits, tru_logits), _rel(ref_logits, tru_logits)
+    assert e_gpu <= max(2 * e_cpu, rtol), f"logits: gpu {e_gpu:.3g} vs cpu {e_cpu:.3g}"
+    assert set(got_grads) == set(tru_grads)
+    for name in tru_grads:
+        e_gpu, e_cpu = _rel(got_grads[name], tru_grads[name]), _rel(ref_grads[name], tru_grads[name])
+        assert e_gpu <= max(2 * e_cpu, rtol), f"{name}: gpu {e_gpu:.3g} vs cpu {e_cpu:.3g}"
+
+
+def test_training_steps_reduce_loss_and_move_router_bias():
+    torch.manual_seed(5)
+    model = TransformerMoe(**CFG).to(torch.bfloat16).cuda().train()
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=1e-2)
+    tokens = torch.randint(0, CFG["vocab_size"], (4, 32), device="cuda")
+    bias0 = [blk.moe.router.expert_bias_E.clone() for blk in model.blocks]
+    losses = []
+    for _ in range(8):
+        logits = model(tokens)
+        loss = F.cross_entropy(logits[:, :-1].reshape(-1, logits.shape[-1]).float(), tokens[:, 1:].reshape(-1))
+        opt.zero_grad(set_to_none=True)
+        loss.backward()
+        opt.step()
+        losses.append(float(loss))
+    assert all(torch.isfinite(torch.tensor(losses)))
+    assert losses[-1] < losses[0], losses
+    assert any(not torch.equal(b0, blk.moe.router.expert_bias_E) for b0, blk in zip(bias0, model.blocks))
