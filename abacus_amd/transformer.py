@@ -143,11 +143,13 @@ class _CausalAttention(torch.autograd.Function):
         q, k, v, p = ctx.saved_tensors
         d_out = d_out.contiguous()
         d_p = torch.bmm(d_out, v.transpose(1, 2).contiguous())
-        d_v = torch.bmm(p.transpose(1, 2).contiguous(), d_out)
+        # dV = P^T dO and dK = dS^T q, formed as (dO^T P)^T and (q^T dS)^T: the
+        # (L, L) matrices stay contiguous and only (L, K) operands are transposed
+        d_v = torch.bmm(d_out.transpose(1, 2).contiguous(), p).transpose(1, 2)
         d_s = torch._softmax_backward_data(d_p, p, -1, p.dtype)  # zero where the mask put -inf
         d_s = d_s / ctx.scale_div
         d_q = torch.bmm(d_s, k)
-        d_k = torch.bmm(d_s.transpose(1, 2).contiguous(), q)
+        d_k = torch.bmm(q.transpose(1, 2).contiguous(), d_s).transpose(1, 2)
         return d_q, d_k, d_v, None
 
 

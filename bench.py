@@ -242,7 +242,7 @@ def main():
         xi = x.requires_grad_(wl.backward)
         out = moe(xi)
         if wl.backward:
-            loss = (out.float() - target.float()).pow(2).mean()
+            loss = torch.nn.functional.mse_loss(out, target)  # mean((y - target)^2)
             loss.backward()
         xi.grad = None
 
