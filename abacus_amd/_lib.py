@@ -29,6 +29,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_hist_len": (_I64, [_I64, _I64]),
     "abacus_moe_router_ws_bytes": (_I64, [_I64, _I64, _I]),
     "abacus_moe_router_wgrad_ws_bytes": (_I64, [_I64, _I64, _I64]),
+    "abacus_moe_down_fwd_ws_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "abacus_moe_load_balancing_ws_bytes": (_I64, [_I64, _I64]),
     "abacus_moe_load_balancing_fwd": (_I, [_P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P, _P]),
     "abacus_moe_load_balancing_bwd": (_I, [_P, _P, _I64, _I64, _F, _I, _P, _P]),
@@ -39,7 +40,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_route_scan": (_I, [_P, _I64, _I64, _I64, _P, _F, _I, _P, _P, _P, _P]),
     "abacus_moe_permute_gather": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
     "abacus_moe_gateup_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
-    "abacus_moe_down_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_down_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _P]),
     "abacus_moe_combine_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_moe_combine_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P]),
     "abacus_moe_down_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),

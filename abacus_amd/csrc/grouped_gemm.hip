@@ -70,6 +70,13 @@ struct GemmArgs {
   int Ndim;                  // output columns (per half for DUAL_B)
   int Kdim;                  // reduction length (per half for DUAL_K); unused for WGRAD
   int tiles_m, tiles_n;      // padded logical tile space of the pipelined kernel
+  // Split tail (pipelined kernel, kinds without a fused epilogue): logical
+  // tiles L >= split_from run as split_parts slices of the reduction, each
+  // writing a row-major fp32 256 x 256 partial to split_ws[(L - split_from) *
+  // split_parts + part]; split_reduce_kernel then adds the slices in order and
+  // writes the tile.  split_parts <= 1: every tile runs whole.
+  int split_from, split_parts;
+  float* split_ws;
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -635,8 +642,27 @@ struct TileId {
 
 __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
-__device__ inline TileId tile_of_block(int b, int G, int MTp, int NTp) {
-  const int L = (b & 7) * (G >> 3) + (b >> 3);
+// Block b of G (a multiple of 8) -> logical tile, XCD-contiguous.
+__device__ inline int xcd_logical(int b, int G) { return (b & 7) * (G >> 3) + (b >> 3); }
+
+// Block b of a kind's G blocks -> (logical tile, slice); slice -1 = whole tile.
+// With a split tail the first split_from blocks are whole tiles; each of the
+// remaining (G - split_from) / 8 per XCD is one slice of a tail tile, and the
+// slices of a tile stay on one XCD.
+__device__ inline void block_to_logical(const GemmArgs& g, int b, int G, int& L, int& part) {
+  if (g.split_parts > 1 && b >= g.split_from) {
+    const int S = g.split_parts;
+    const int per_xcd = (G - g.split_from) / (8 * S);  // tail tiles per XCD
+    const int u = b - g.split_from, v = u >> 3;
+    L = g.split_from + (u & 7) * per_xcd + v / S;
+    part = v % S;
+  } else {
+    L = xcd_logical(b, g.split_parts > 1 ? g.split_from : G);
+    part = -1;
+  }
+}
+
+__device__ inline TileId tile_of_logical(int L, int MTp, int NTp) {
   const int per = MTp * NTp;
   TileId t;
   t.e = L / per;
@@ -664,8 +690,11 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // ---------------- tile -> (expert, rows, columns) ----------------
-  // 1-D space of G = (E or 1) x tiles_m x tiles_n blocks
-  const TileId tl = tile_of_block(b, G, g.tiles_m, g.tiles_n);
+  // 1-D space of G = (E or 1) x tiles_m x tiles_n logical tiles (more blocks
+  // than that with a split tail)
+  int L, part;
+  block_to_logical(g, b, G, L, part);
+  const TileId tl = tile_of_logical(L, g.tiles_m, g.tiles_n);
   const int n0 = tl.nt * BNH;
   if (n0 >= g.Ndim) return;
   int e = -1, row0 = 0, row_end = 0, k_len = 0;
@@ -705,7 +734,14 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     if (KT::DUAL_B) B1 += (int64_t)seg0 * g.ldb;
   }
   const int ktiles_half = (k_len + BK - 1) / BK;
-  const int ktiles = KT::DUAL_K ? 2 * ktiles_half : ktiles_half;
+  const int ktiles_all = KT::DUAL_K ? 2 * ktiles_half : ktiles_half;
+  // a slice of a split tile runs k-tiles kbase .. kbase + ktiles - 1
+  int kbase = 0, ktiles = ktiles_all;
+  if (part >= 0) {
+    const int per = (ktiles_all + g.split_parts - 1) / g.split_parts;
+    kbase = part * per;
+    ktiles = max(0, min(per, ktiles_all - kbase));
+  }
   const int a_lim = KT::WGRAD ? g.Mdim : row_end;
 
   // wave index as a scalar so the DMA destinations are computed in SGPRs
@@ -722,6 +758,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   int dma_k0 = 0;
   auto prep = [&](int kt) __attribute__((always_inline)) {
     dma_stage = lds + (kt % STAGES) * STAGE_BYTES;
+    kt += kbase;  // the k-tile within the whole reduction
     const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
     if (KT::DUAL_K && half != half_set) {  // second half of the concatenated k range
       sa.setup(A1, nullptr, g.lda, row0, a_lim, wave, lane);
@@ -845,6 +882,20 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     for (; kt + STAGES < ktiles; ++kt) ktile(kt, true, true);
     for (; kt + 1 < ktiles; ++kt) ktile(kt, true, false);
     ktile(kt, false, false);
+  }
+  if (part >= 0) {
+    // a slice of a split tile: its fp32 partial, row-major, for split_reduce_kernel
+    float* ws = g.split_ws + ((int64_t)(L - g.split_from) * g.split_parts + part) * (BM * BN);
+    const int rl = lane & 31, ch = 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq)
+          *reinterpret_cast<float4*>(ws + (wm * WTM + i * 32 + rl) * BN + b_col(j) + 8 * gq + ch) =
+              make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2], acc[i][j][4 * gq + 3]);
+    return;
   }
   __syncthreads();  // all fragment reads done before the C tile overwrites the stages
 
@@ -971,6 +1022,49 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_pair_kernel(GemmArgs ga, Gemm
   else gemm_tile<KB>(gb, (int)blockIdx.x - ga_blocks, (int)gridDim.x - ga_blocks, lds);
 }
 
+// Adds the slices of each split tail tile in slice order and writes the tile
+// (kinds whose epilogue is a plain store of the bf16-rounded product).
+template <int KIND>
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
+  using KT = KindTraits<KIND>;
+  static_assert(!KT::WGRAD && !KT::DUAL_B && KIND != kDownDgrad, "plain-store epilogues only");
+  const int L = g.split_from + blockIdx.x;
+  const TileId tl = tile_of_logical(L, g.tiles_m, g.tiles_n);
+  const int n0 = tl.nt * BN;
+  if (n0 >= g.Ndim) return;
+  int row0 = 0, row_end = 0, acc_tiles = 0;
+  bool found = false;
+  for (int i = 0; i < g.E && !found; ++i) {
+    const int a = g.offsets[i], b = g.offsets[i + 1];
+    const int nt = (b - a + BM - 1) / BM;
+    if (tl.mt < acc_tiles + nt) {
+      row0 = a + (tl.mt - acc_tiles) * BM;
+      row_end = b;
+      found = true;
+    }
+    acc_tiles += nt;
+  }
+  if (!found) return;
+  const float* ws = g.split_ws + (int64_t)blockIdx.x * g.split_parts * (BM * BN);
+  constexpr int CV = BN / 8;
+  for (int v = threadIdx.x; v < BM * CV; v += 256) {
+    const int r = v / CV, c = (v % CV) * 8;
+    const int row = row0 + r, col = n0 + c;
+    if (row >= row_end || col >= g.Ndim) continue;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < g.split_parts; ++p) {
+      const float4 lo = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c);
+      const float4 hi = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c + 4);
+      s[0] += lo.x; s[1] += lo.y; s[2] += lo.z; s[3] += lo.w;
+      s[4] += hi.x; s[5] += hi.y; s[6] += hi.z; s[7] += hi.w;
+    }
+    Vec16 out;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) out.w[w] = pack_bf16x2(s[2 * w], s[2 * w + 1]);
+    st16((uint16_t*)g.c0 + (int64_t)row * g.ldc + col, out);
+  }
+}
+
 }  // namespace pipe
 
 // Tile configuration per (dtype, kind).
@@ -1032,6 +1126,67 @@ int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
   return 0;
 }
 
+// CUs of the current device (one work-group of the pipelined kernel fits a
+// CU); 256 (MI355X) when no device answers, so that workspace queries work on
+// a host without a GPU.
+inline int cu_count() {
+  static int cached = 0;
+  if (cached == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cached = n;
+    else
+      cached = 256;
+  }
+  return cached;
+}
+
+// Split-tail plan of a row-grouped kind: the tiles of the whole rounds that
+// certainly exist (ceil(R / BM) row tiles, whatever the experts' raggedness)
+// run whole; the rest of the logical space runs as kSplitParts slices, so the
+// last, partial round takes a third of a tile's time.  ws bytes: 0 = no split.
+constexpr int kSplitParts = 3;
+struct SplitPlan {
+  int from = 0, parts = 1, tail = 0;
+  int64_t ws_bytes() const { return parts > 1 ? (int64_t)tail * parts * pipe::BM * pipe::BN * 4 : 0; }
+};
+
+template <int KIND>
+SplitPlan plan_split(const GemmArgs& g, int R) {
+  static_assert(!KindTraits<KIND>::WGRAD && !KindTraits<KIND>::DUAL_B, "row-grouped plain-store kinds");
+  SplitPlan p;
+  GemmArgs t = g;
+  const int64_t total = pipe_grid<KIND>(t, R);
+  const int64_t real_n = (g.Ndim + pipe::BN - 1) / pipe::BN;
+  const int64_t whole = (int64_t)((R + pipe::BM - 1) / pipe::BM) * real_n;
+  const int cus = cu_count();
+  int64_t from = whole / cus * cus;
+  from -= from % 8;
+  if (from <= 0 || from >= total) return p;
+  p.from = (int)from;
+  p.parts = kSplitParts;
+  p.tail = (int)(total - from);
+  return p;
+}
+
+template <int KIND>
+int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws, hipStream_t s, const char* name) {
+  GemmArgs ga = g;
+  const int64_t total = pipe_grid<KIND>(ga, R);
+  if (total == 0) return 0;
+  ga.split_from = plan.from;
+  ga.split_parts = plan.parts;
+  ga.split_ws = ws;
+  const int64_t blocks = plan.from + (int64_t)plan.parts * plan.tail;
+  ABACUS_CHECK_ARG(blocks < (1ll << 31), "%s: tile grid too large", name);
+  hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
+  ABACUS_CHECK_LAUNCH(name);
+  hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail), dim3(256), 0, s, ga);
+  ABACUS_CHECK_LAUNCH(name);
+  return 0;
+}
+
 // Kinds KA (the long tiles) and KB in one launch.
 template <int KA, int KB>
 int launch_pipe_pair(const GemmArgs& a, int Ra, const GemmArgs& b, int Rb, hipStream_t s, const char* name) {
@@ -1089,6 +1244,25 @@ int check_gemm_shape(int64_t R, int64_t D, int64_t M, int64_t E, int dtype) {
   ABACUS_CHECK_ARG(M >= 1 && M % vec == 0 && M < (1ll << 31), "hidden_dim %lld must be a positive multiple of %d",
                    (long long)M, vec);
   return 0;
+}
+
+// Y = H . Wd[e]: A = H (k-contiguous rows of length M), B(k=m, j=d) = Wd[e][m][d].
+GemmArgs args_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t* offsets_E1, int64_t R, int64_t M,
+                       int64_t D, int64_t E, void* y_RD) {
+  GemmArgs g{};
+  g.a0 = h_RM;
+  g.b0 = w_down_EMD;
+  g.lda = M;
+  g.ldb = D;
+  g.b_estride = M * D;
+  g.c0 = y_RD;
+  g.ldc = D;
+  g.offsets = offsets_E1;
+  g.E = (int)E;
+  g.Mdim = (int)R;
+  g.Ndim = (int)D;
+  g.Kdim = (int)M;
+  return g;
 }
 
 // dH = dY . Wd[e]^T with the SwiGLU backward fused: B(k=d, j=m) = Wd[e][m][d],
@@ -1203,23 +1377,23 @@ int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const v
   return dispatch_gemm<kGateUpFwd>(dtype, g, (int)R, (hipStream_t)stream, "gateup_fwd");
 }
 
+int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype) {
+  if (check_gemm_shape(R, D, M, E, dtype) || R == 0) return 0;
+  const GemmArgs g = args_down_fwd(nullptr, nullptr, nullptr, R, M, D, E, nullptr);
+  if (!pipe_ok<kDownFwd>(dtype, g)) return 0;
+  return plan_split<kDownFwd>(g, (int)R).ws_bytes();
+}
+
 int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t* offsets_E1, int64_t R, int64_t M,
-                        int64_t D, int64_t E, int dtype, void* y_RD, void* stream) {
+                        int64_t D, int64_t E, int dtype, void* y_RD, void* ws, int64_t ws_bytes, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   if (R == 0) return 0;
-  GemmArgs g{};
-  g.a0 = h_RM;
-  g.b0 = w_down_EMD;
-  g.lda = M;
-  g.ldb = D;
-  g.b_estride = M * D;
-  g.c0 = y_RD;
-  g.ldc = D;
-  g.offsets = offsets_E1;
-  g.E = (int)E;
-  g.Mdim = (int)R;
-  g.Ndim = (int)D;
-  g.Kdim = (int)M;
+  const GemmArgs g = args_down_fwd(h_RM, w_down_EMD, offsets_E1, R, M, D, E, y_RD);
+  if (pipe_ok<kDownFwd>(dtype, g) && ws != nullptr) {
+    const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);
+    if (plan.parts > 1 && ws_bytes >= plan.ws_bytes())
+      return launch_pipe_split<kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd");
+  }
   return dispatch_gemm<kDownFwd>(dtype, g, (int)R, (hipStream_t)stream, "down_fwd");
 }
 

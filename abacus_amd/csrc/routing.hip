@@ -579,15 +579,77 @@ __global__ __launch_bounds__(256) void router_wgrad_partial_kernel(const T* __re
   }
 }
 
+// dW_DE partials for E <= EMAX: each thread owns 4 consecutive columns and
+// keeps their E accumulators in registers.  A token's K (expert, dlogit)
+// pairs are the same for every thread of the block (scalar loads); they are
+// expanded to a dense coefficient row, so the accumulator index is a
+// compile-time constant.  Tokens are added in order within a chunk.
+template <typename T, int EMAX>
+__global__ __launch_bounds__(256) void router_wgrad_partial_reg_kernel(const T* __restrict__ x,
+                                                                       const float* __restrict__ dlogit,
+                                                                       const int32_t* __restrict__ idx, int T_, int D,
+                                                                       int E, int K, int chunk,
+                                                                       float* __restrict__ partial) {
+  constexpr int CPT = 4;
+  const int d0 = (blockIdx.x * 256 + threadIdx.x) * CPT;
+  const int c = blockIdx.y;
+  const int ta = c * chunk;
+  const int tb = min(T_, ta + chunk);
+  float acc[EMAX][CPT];
+#pragma unroll
+  for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) acc[e][j] = 0.f;
+  if (d0 < D) {
+#pragma unroll 4
+    for (int t = ta; t < tb; ++t) {
+      float xv[CPT];
+      if constexpr (sizeof(T) == 2) {
+        const uint2 w = *reinterpret_cast<const uint2*>(x + (int64_t)t * D + d0);
+        xv[0] = bits_f32(w.x << 16);
+        xv[1] = bits_f32(w.x & 0xffff0000u);
+        xv[2] = bits_f32(w.y << 16);
+        xv[3] = bits_f32(w.y & 0xffff0000u);
+      } else {
+        const float4 w = *reinterpret_cast<const float4*>(x + (int64_t)t * D + d0);
+        xv[0] = w.x;
+        xv[1] = w.y;
+        xv[2] = w.z;
+        xv[3] = w.w;
+      }
+      float coef[EMAX];
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) coef[e] = 0.f;
+      for (int k = 0; k < K; ++k) {
+        const int ek = idx[(int64_t)t * K + k];
+        const float wk = dlogit[(int64_t)t * K + k];
+#pragma unroll
+        for (int e = 0; e < EMAX; ++e) coef[e] = ek == e ? coef[e] + wk : coef[e];
+      }
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e)
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) acc[e][j] += xv[j] * coef[e];
+    }
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e)
+      if (e < E) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) partial[((int64_t)c * E + e) * D + d0 + j] = acc[e][j];
+      }
+  }
+}
+
 template <typename T>
 __global__ void router_wgrad_reduce_kernel(const float* __restrict__ partial, int nchunks, int D, int E,
                                            T* __restrict__ dw) {
+  // d fastest across threads: the chunk partials are read in full rows
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= (int64_t)D * E) return;
-  const int d = (int)(i / E), e = (int)(i % E);
+  const int e = (int)(i / D), d = (int)(i % D);
   float s = 0.f;
   for (int c = 0; c < nchunks; ++c) s += partial[((int64_t)c * E + e) * D + d];
-  dw[i] = from_f32<T>(s);
+  dw[(int64_t)d * E + e] = from_f32<T>(s);
 }
 
 // Standalone Router.update_bias(indices) (router.py:57-70).
@@ -806,8 +868,13 @@ int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, con
   return 0;
 }
 
-static void router_wgrad_plan(int64_t T, int64_t D, int* chunk, int* nchunks) {
-  const int64_t dblocks = (D + 255) / 256;
+// The register path (4 columns per thread, E <= 16) needs D % 4 == 0; the
+// column path takes any D and E.
+static bool router_wgrad_reg_path(int64_t D, int64_t E) { return E <= 16 && D % 4 == 0; }
+
+static void router_wgrad_plan(int64_t T, int64_t D, bool reg, int* chunk, int* nchunks) {
+  const int64_t cols_per_block = reg ? 1024 : 256;
+  const int64_t dblocks = (D + cols_per_block - 1) / cols_per_block;
   int64_t want = std::max<int64_t>(1, 512 / dblocks);
   int64_t nc = std::min<int64_t>(want, std::max<int64_t>(1, (T + 63) / 64));
   int64_t ch = (T + nc - 1) / nc;
@@ -819,7 +886,7 @@ static void router_wgrad_plan(int64_t T, int64_t D, int* chunk, int* nchunks) {
 
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E) {
   int chunk, nchunks;
-  router_wgrad_plan(T, D, &chunk, &nchunks);
+  router_wgrad_plan(T, D, router_wgrad_reg_path(D, E), &chunk, &nchunks);
   return (int64_t)nchunks * E * D * 4;
 }
 
@@ -829,15 +896,30 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
   ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
   ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
   hipStream_t s = (hipStream_t)stream;
+  const bool reg = router_wgrad_reg_path(D, E);
   int chunk, nchunks;
-  router_wgrad_plan(T, D, &chunk, &nchunks);
-  const dim3 g1((unsigned)((D + 255) / 256), (unsigned)nchunks);
+  router_wgrad_plan(T, D, reg, &chunk, &nchunks);
   const int g2 = (int)((D * E + 255) / 256);
   // With T == 0 the partial kernel visits no tokens and writes zero partials.
-  if (dtype == kBF16) {
+  if (reg) {
+    const dim3 g1((unsigned)((D + 1023) / 1024), (unsigned)nchunks);
+#define ABACUS_WGRAD_REG(TT, EM)                                                                               \
+  hipLaunchKernelGGL((router_wgrad_partial_reg_kernel<TT, EM>), g1, dim3(256), 0, s, (const TT*)x_TD, dlogit_TK, \
+                     idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws)
+    if (dtype == kBF16) {
+      if (E <= 8) ABACUS_WGRAD_REG(uint16_t, 8);
+      else ABACUS_WGRAD_REG(uint16_t, 16);
+    } else {
+      if (E <= 8) ABACUS_WGRAD_REG(float, 8);
+      else ABACUS_WGRAD_REG(float, 16);
+    }
+#undef ABACUS_WGRAD_REG
+  } else if (dtype == kBF16) {
+    const dim3 g1((unsigned)((D + 255) / 256), (unsigned)nchunks);
     hipLaunchKernelGGL(router_wgrad_partial_kernel<uint16_t>, g1, dim3(256), 0, s, (const uint16_t*)x_TD,
                        dlogit_TK, idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
   } else {
+    const dim3 g1((unsigned)((D + 255) / 256), (unsigned)nchunks);
     hipLaunchKernelGGL(router_wgrad_partial_kernel<float>, g1, dim3(256), 0, s, (const float*)x_TD, dlogit_TK,
                        idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
   }

@@ -164,7 +164,9 @@ class _MoEFunction(torch.autograd.Function):
             ptr(gate), ptr(up), ptr(h), s,
         )
         y = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
-        call("abacus_moe_down_fwd", ptr(h), ptr(w_down), ptr(offsets), R, M, D, E, dt, ptr(y), s)
+        ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, E, dt)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+        call("abacus_moe_down_fwd", ptr(h), ptr(w_down), ptr(offsets), R, M, D, E, dt, ptr(y), ptr(ws), ws_bytes, s)
         out = torch.empty(T, D, dtype=x_TD.dtype, device=dev)
         call("abacus_moe_combine_fwd", ptr(y), ptr(weights), ptr(idx32), ptr(pos), T, D, K, dt, ptr(out), s)
         if need_grad:

@@ -43,6 +43,8 @@ int64_t abacus_moe_hist_len(int64_t T, int64_t E);
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
 /* bytes of the fp32 partial-sum scratch used by router_wgrad. */
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E);
+/* bytes of the split-tail workspace of down_fwd (0: that shape runs no split). */
+int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype);
 /* bytes of the per-block partial sums and counts used by load_balancing_fwd. */
 int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E);
 
@@ -80,9 +82,14 @@ int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const v
                           const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
                           void* gate_RM, void* up_RM, void* h_RM, void* stream);
 
-/* Replaces moe.py:80: y = h @ w_down[e] for every expert. */
+/* Replaces moe.py:80: y = h @ w_down[e] for every expert.  With a workspace of
+ * abacus_moe_down_fwd_ws_bytes bytes (bf16), the tiles beyond the whole rounds
+ * of the GPU's CUs run as slices of the reduction, whose fp32 partials the
+ * workspace holds; ws = NULL (or too small) runs every tile whole.  Either way
+ * the same products are summed, in a fixed order: repeated calls agree bit
+ * for bit. */
 int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t* offsets_E1, int64_t R, int64_t M,
-                        int64_t D, int64_t E, int dtype, void* y_RD, void* stream);
+                        int64_t D, int64_t E, int dtype, void* y_RD, void* ws, int64_t ws_bytes, void* stream);
 
 /* Replaces moe.py:81-85: out[t] = sum over the token's experts (ascending)
  * of y[pos(t,k)] * weights_TK[t,k]. */

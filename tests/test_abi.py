@@ -60,7 +60,7 @@ def test_abi_version_and_queries():
         ("abacus_moe_permute_gather", (None, None, None, 16, 12, 8, 2, 1, None, None, None, None), "dim"),
         ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 2, 1.0, 7) + (None,) * 8, "dtype"),
         ("abacus_moe_gateup_fwd", (None, None, None, None, 16, 64, 30, 8, 0, None, None, None, None), "hidden_dim"),
-        ("abacus_moe_down_fwd", (None, None, None, 16, 64, 64, 0, 0, None, None), "n_experts"),
+        ("abacus_moe_down_fwd", (None, None, None, 16, 64, 64, 0, 0, None, None, 0, None), "n_experts"),
     ],
 )
 def test_rejected_arguments_raise_with_message(name, args, msg):

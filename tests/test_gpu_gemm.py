@@ -127,3 +127,36 @@ def test_pair_results_match_fp64_products():
                 continue
             err = (f(got) - want).norm() / max(want.norm().item(), 1e-30)
             assert err < 1e-2, f"expert {e} {name}: relative error {err:.3g}"
+
+
+def test_down_fwd_split_tail():
+    """Tiles past the GPU's whole rounds run as reduction slices plus a reduce kernel: same product."""
+    counts, D, M = [1100, 950, 1030, 1010, 990, 1060, 1000, 1052], 4096, 512
+    o = _operands(counts, D, M, torch.bfloat16, seed=14)
+    E, R = o["E"], o["R"]
+    h, w_down = o["h"], torch.randn(E, M, D, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
+    w_down = (w_down * 0.05).to(torch.bfloat16)
+    s = _lib.stream_of(torch.device("cuda"))
+    ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, E, 1)
+    assert ws_bytes > 0, "this shape has a partial last round on any GPU of up to 256 CUs"
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    outs = []
+    for use_ws in (True, True, False):
+        y = torch.full((R, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+        call("abacus_moe_down_fwd", ptr(h), ptr(w_down), ptr(o["offsets"]), R, M, D, E, 1, ptr(y),
+             ptr(ws) if use_ws else None, ws_bytes if use_ws else 0, s)
+        outs.append(y)
+    torch.cuda.synchronize()
+    split1, split2, whole = outs
+    assert torch.equal(split1, split2), "repeated split calls differ"
+    assert not torch.isnan(split1).any()
+    # only the fp32 summation order differs: a few elements one bf16 rounding apart
+    diff = (split1.float() - whole.float()).abs()
+    assert float(diff.max()) <= 2 ** -7 * float(whole.float().abs().max())
+    assert float((diff > 0).float().mean()) < 0.05
+    off = o["offsets"].tolist()
+    for e in range(E):
+        a, b = off[e], off[e + 1]
+        want = h[a:b].float() @ w_down[e].float()
+        err = float((split1[a:b].float() - want).norm() / want.norm())
+        assert err < 1e-2, f"expert {e}: relative error {err:.3g}"
