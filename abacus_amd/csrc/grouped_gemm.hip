@@ -70,12 +70,14 @@ struct GemmArgs {
   int Ndim;                  // output columns (per half for DUAL_B)
   int Kdim;                  // reduction length (per half for DUAL_K); unused for WGRAD
   int tiles_m, tiles_n;      // padded logical tile space of the pipelined kernel
-  // Split tail (pipelined kernel, kinds without a fused epilogue): logical
-  // tiles L >= split_from run as split_parts slices of the reduction, each
-  // writing a row-major fp32 256 x 256 partial to split_ws[(L - split_from) *
-  // split_parts + part]; split_reduce_kernel then adds the slices in order and
-  // writes the tile.  split_parts <= 1: every tile runs whole.
-  int split_from, split_parts;
+  // Split tail (pipelined kernel, row-grouped kinds without a fused
+  // epilogue): of the `total` real tiles, the largest multiple of split_cus
+  // run whole in blocks [0, split_from); the rest (fewer than split_cus) run
+  // as up to split_parts slices of the reduction in the blocks after that,
+  // each writing a row-major fp32 256 x 256 partial to split_ws; then
+  // split_reduce_kernel adds the slices in order and writes the tiles.
+  // split_parts <= 1: every tile runs whole.
+  int split_from, split_parts, split_cus;
   float* split_ws;
 };
 
@@ -645,21 +647,64 @@ __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b *
 // Block b of G (a multiple of 8) -> logical tile, XCD-contiguous.
 __device__ inline int xcd_logical(int b, int G) { return (b & 7) * (G >> 3) + (b >> 3); }
 
-// Block b of a kind's G blocks -> (logical tile, slice); slice -1 = whole tile.
-// With a split tail the first split_from blocks are whole tiles; each of the
-// remaining (G - split_from) / 8 per XCD is one slice of a tail tile, and the
-// slices of a tile stay on one XCD.
-__device__ inline void block_to_logical(const GemmArgs& g, int b, int G, int& L, int& part) {
-  if (g.split_parts > 1 && b >= g.split_from) {
-    const int S = g.split_parts;
-    const int per_xcd = (G - g.split_from) / (8 * S);  // tail tiles per XCD
-    const int u = b - g.split_from, v = u >> 3;
-    L = g.split_from + (u & 7) * per_xcd + v / S;
-    part = v % S;
+// Row-grouped kinds (the expert's rows are the output rows): the real row
+// tiles are counted from the offsets, and the real tiles (x tiles_n column
+// tiles) are numbered in the same GM x GN groups, the last group of rows
+// possibly short.  Each XCD takes an equal, contiguous share of them, so no
+// XCD is left with the padding of the host's upper bound.
+__device__ inline int count_row_tiles(const GemmArgs& g) {
+  int n = 0;
+  for (int i = 0; i < g.E; ++i) n += (g.offsets[i + 1] - g.offsets[i] + BM - 1) / BM;
+  return n;
+}
+
+__device__ inline void row_tile(int r, int mt_real, int NTp, int& mt, int& nt) {
+  const int full = (mt_real / GM) * GM * NTp;  // tiles in whole groups of GM rows
+  if (r < full) {
+    const int gi = r / (GM * GN), w = r % (GM * GN);
+    const int ngn = NTp / GN;
+    mt = (gi / ngn) * GM + w / GN;
+    nt = (gi % ngn) * GN + w % GN;
   } else {
-    L = xcd_logical(b, g.split_parts > 1 ? g.split_from : G);
-    part = -1;
+    const int rows = mt_real % GM;  // the short last group (nonzero when r >= full)
+    const int r2 = r - full;
+    mt = (mt_real / GM) * GM + (r2 % (rows * GN)) / GN;
+    nt = (r2 / (rows * GN)) * GN + r2 % GN;
   }
+}
+
+// Slices per tile of a split tail of `tail` tiles: enough to cover the CUs,
+// at most split_parts.
+__device__ inline int split_slices(const GemmArgs& g, int tail) {
+  return tail <= 0 ? 1 : min(g.split_parts, max(1, g.split_cus / tail));
+}
+
+// Block b -> (real tile r, slice; -1 = whole).  False: the block has no tile.
+__device__ inline bool block_to_row_tile(const GemmArgs& g, int b, int total, int& r, int& part) {
+  part = -1;
+  if (g.split_parts > 1) {
+    const int whole = total / g.split_cus * g.split_cus;
+    if (b < g.split_from) {
+      const int per = whole / 8;  // split_cus is a multiple of 8
+      const int j = b >> 3;
+      if (j >= per) return false;
+      r = (b & 7) * per + j;
+      return true;
+    }
+    const int tail = total - whole, S = split_slices(g, tail);
+    const int per_t = (tail + 7) / 8;
+    const int u = b - g.split_from, x = u & 7, j = u >> 3;
+    const int lo = whole + x * per_t, hi = min(whole + (x + 1) * per_t, total);
+    if (j >= (hi - lo) * S) return false;
+    r = lo + j / S;
+    part = S > 1 ? j % S : -1;
+    return true;
+  }
+  const int per = (total + 7) / 8;
+  const int j = b >> 3;
+  if (j >= per) return false;
+  r = (b & 7) * per + j;
+  return r < total;
 }
 
 __device__ inline TileId tile_of_logical(int L, int MTp, int NTp) {
@@ -690,14 +735,22 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // ---------------- tile -> (expert, rows, columns) ----------------
-  // 1-D space of G = (E or 1) x tiles_m x tiles_n logical tiles (more blocks
-  // than that with a split tail)
-  int L, part;
-  block_to_logical(g, b, G, L, part);
-  const TileId tl = tile_of_logical(L, g.tiles_m, g.tiles_n);
-  const int n0 = tl.nt * BNH;
+  int e = -1, row0 = 0, row_end = 0, k_len = 0, n0 = 0;
+  int part = -1, slot = 0;  // slice of a split tail tile, its workspace slot
+  TileId tl;
+  if (!KT::WGRAD) {
+    const int mt_real = count_row_tiles(g);
+    const int total = mt_real * g.tiles_n;
+    int r;
+    if (!block_to_row_tile(g, b, total, r, part)) return;
+    row_tile(r, mt_real, g.tiles_n, tl.mt, tl.nt);
+    if (part >= 0) slot = r - total / g.split_cus * g.split_cus;
+  } else {
+    // per-expert tile space (E x tiles_m x tiles_n), XCD-contiguous
+    tl = tile_of_logical(xcd_logical(b, G), g.tiles_m, g.tiles_n);
+  }
+  n0 = tl.nt * BNH;
   if (n0 >= g.Ndim) return;
-  int e = -1, row0 = 0, row_end = 0, k_len = 0;
   if (!KT::WGRAD) {
     int acc_tiles = 0;
     const int bx = tl.mt;
@@ -738,7 +791,8 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // a slice of a split tile runs k-tiles kbase .. kbase + ktiles - 1
   int kbase = 0, ktiles = ktiles_all;
   if (part >= 0) {
-    const int per = (ktiles_all + g.split_parts - 1) / g.split_parts;
+    const int S = split_slices(g, count_row_tiles(g) * g.tiles_n % g.split_cus);
+    const int per = (ktiles_all + S - 1) / S;
     kbase = part * per;
     ktiles = max(0, min(per, ktiles_all - kbase));
   }
@@ -885,7 +939,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   }
   if (part >= 0) {
     // a slice of a split tile: its fp32 partial, row-major, for split_reduce_kernel
-    float* ws = g.split_ws + ((int64_t)(L - g.split_from) * g.split_parts + part) * (BM * BN);
+    float* ws = g.split_ws + ((int64_t)slot * g.split_parts + part) * (BM * BN);
     const int rl = lane & 31, ch = 4 * (lane >> 5);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -1023,28 +1077,32 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_pair_kernel(GemmArgs ga, Gemm
 }
 
 // Adds the slices of each split tail tile in slice order and writes the tile
-// (kinds whose epilogue is a plain store of the bf16-rounded product).
+// (kinds whose epilogue is a plain store of the bf16-rounded product).  Block
+// i serves tail tile i.
 template <int KIND>
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   using KT = KindTraits<KIND>;
   static_assert(!KT::WGRAD && !KT::DUAL_B && KIND != kDownDgrad, "plain-store epilogues only");
-  const int L = g.split_from + blockIdx.x;
-  const TileId tl = tile_of_logical(L, g.tiles_m, g.tiles_n);
+  const int mt_real = count_row_tiles(g);
+  const int total = mt_real * g.tiles_n;
+  const int whole = total / g.split_cus * g.split_cus;
+  const int S = split_slices(g, total - whole);
+  if (S <= 1 || (int)blockIdx.x >= total - whole) return;
+  TileId tl;
+  row_tile(whole + (int)blockIdx.x, mt_real, g.tiles_n, tl.mt, tl.nt);
   const int n0 = tl.nt * BN;
   if (n0 >= g.Ndim) return;
   int row0 = 0, row_end = 0, acc_tiles = 0;
-  bool found = false;
-  for (int i = 0; i < g.E && !found; ++i) {
+  for (int i = 0; i < g.E; ++i) {
     const int a = g.offsets[i], b = g.offsets[i + 1];
     const int nt = (b - a + BM - 1) / BM;
     if (tl.mt < acc_tiles + nt) {
       row0 = a + (tl.mt - acc_tiles) * BM;
       row_end = b;
-      found = true;
+      break;
     }
     acc_tiles += nt;
   }
-  if (!found) return;
   const float* ws = g.split_ws + (int64_t)blockIdx.x * g.split_parts * (BM * BN);
   constexpr int CV = BN / 8;
   for (int v = threadIdx.x; v < BM * CV; v += 256) {
@@ -1052,7 +1110,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
     const int row = row0 + r, col = n0 + c;
     if (row >= row_end || col >= g.Ndim) continue;
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < g.split_parts; ++p) {
+    for (int p = 0; p < S; ++p) {
       const float4 lo = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c);
       const float4 hi = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c + 4);
       s[0] += lo.x; s[1] += lo.y; s[2] += lo.z; s[3] += lo.w;
@@ -1142,14 +1200,15 @@ inline int cu_count() {
   return cached;
 }
 
-// Split-tail plan of a row-grouped kind: the tiles of the whole rounds that
-// certainly exist (ceil(R / BM) row tiles, whatever the experts' raggedness)
-// run whole; the rest of the logical space runs as kSplitParts slices, so the
-// last, partial round takes a third of a tile's time.  ws bytes: 0 = no split.
+// Split-tail plan of a row-grouped kind.  The device knows the real tile
+// count; the host sizes the grid for any count up to its upper bound: the
+// whole-tile blocks for the largest multiple of the CU count the bound
+// allows, and kSplitParts slices of fewer than CU-count tail tiles.
 constexpr int kSplitParts = 3;
 struct SplitPlan {
-  int from = 0, parts = 1, tail = 0;
-  int64_t ws_bytes() const { return parts > 1 ? (int64_t)tail * parts * pipe::BM * pipe::BN * 4 : 0; }
+  int whole_blocks = 0, slice_blocks = 0, tail_max = 0;
+  bool on() const { return slice_blocks > 0; }
+  int64_t ws_bytes() const { return on() ? (int64_t)tail_max * kSplitParts * pipe::BM * pipe::BN * 4 : 0; }
 };
 
 template <int KIND>
@@ -1157,32 +1216,27 @@ SplitPlan plan_split(const GemmArgs& g, int R) {
   static_assert(!KindTraits<KIND>::WGRAD && !KindTraits<KIND>::DUAL_B, "row-grouped plain-store kinds");
   SplitPlan p;
   GemmArgs t = g;
-  const int64_t total = pipe_grid<KIND>(t, R);
-  const int64_t real_n = (g.Ndim + pipe::BN - 1) / pipe::BN;
-  const int64_t whole = (int64_t)((R + pipe::BM - 1) / pipe::BM) * real_n;
+  const int64_t total_max = pipe_grid<KIND>(t, R);
+  if (total_max == 0) return p;
   const int cus = cu_count();
-  int64_t from = whole / cus * cus;
-  from -= from % 8;
-  if (from <= 0 || from >= total) return p;
-  p.from = (int)from;
-  p.parts = kSplitParts;
-  p.tail = (int)(total - from);
+  p.whole_blocks = (int)(total_max / cus * cus);
+  p.tail_max = (int)std::min<int64_t>(cus - 1, total_max);
+  p.slice_blocks = cus * kSplitParts;
   return p;
 }
 
 template <int KIND>
 int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws, hipStream_t s, const char* name) {
   GemmArgs ga = g;
-  const int64_t total = pipe_grid<KIND>(ga, R);
-  if (total == 0) return 0;
-  ga.split_from = plan.from;
-  ga.split_parts = plan.parts;
+  if (pipe_grid<KIND>(ga, R) == 0) return 0;
+  ga.split_from = plan.whole_blocks;
+  ga.split_parts = kSplitParts;
+  ga.split_cus = cu_count();
   ga.split_ws = ws;
-  const int64_t blocks = plan.from + (int64_t)plan.parts * plan.tail;
-  ABACUS_CHECK_ARG(blocks < (1ll << 31), "%s: tile grid too large", name);
+  const int64_t blocks = (int64_t)plan.whole_blocks + plan.slice_blocks;
   hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
   ABACUS_CHECK_LAUNCH(name);
-  hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail), dim3(256), 0, s, ga);
+  hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail_max), dim3(256), 0, s, ga);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
@@ -1391,7 +1445,7 @@ int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t*
   const GemmArgs g = args_down_fwd(h_RM, w_down_EMD, offsets_E1, R, M, D, E, y_RD);
   if (pipe_ok<kDownFwd>(dtype, g) && ws != nullptr) {
     const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);
-    if (plan.parts > 1 && ws_bytes >= plan.ws_bytes())
+    if (plan.on() && ws_bytes >= plan.ws_bytes())
       return launch_pipe_split<kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd");
   }
   return dispatch_gemm<kDownFwd>(dtype, g, (int)R, (hipStream_t)stream, "down_fwd");
