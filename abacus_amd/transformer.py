@@ -14,10 +14,13 @@ reference's:
   TransformerMoe       abacus/transformer_moe.py:17-75
 
 The MoE layer inside each block is abacus_amd.moe.MoE (the HIP path).  The
-rest runs on torch.  Causal attention is materialised like the reference's
-(scores, mask, softmax, weighted sum), written as one autograd function whose
-batched products all take contiguous operands.  Tensor, sequence and context
-parallelism with more than one process are not part of this build.
+rest runs on torch.  Causal attention on the GPU is torch's fused kernel
+(flash / memory-efficient: the (L, L) scores never reach HBM, and stay fp32
+where the reference rounds them to the activation dtype); on the CPU, or for
+inputs no fused kernel takes, it is materialised like the reference's (scores,
+mask, softmax, weighted sum) as one autograd function whose batched products
+all take contiguous operands.  Tensor, sequence and context parallelism with
+more than one process are not part of this build.
 """
 
 from __future__ import annotations
@@ -153,6 +156,38 @@ class _CausalAttention(torch.autograd.Function):
         return d_q, d_k, d_v, None
 
 
+# Fused causal attention on the GPU: torch's flash / memory-efficient
+# kernels (scores and probabilities stay on chip, in fp32), never its
+# materializing math path.  Inputs neither kernel takes fall back to
+# _CausalAttention; the verdict is kept per (dtype, head_dim).
+_FUSED_BACKENDS = None
+_fused_ok: dict = {}
+
+
+def _fused_causal_attention(q, k, v):
+    """softmax(mask(q k^T / sqrt(K))) v for (B, H, L, K) q, k, v, or None."""
+    global _FUSED_BACKENDS
+    key = (q.dtype, q.shape[-1])
+    if _fused_ok.get(key) is False or not (q.dtype == k.dtype == v.dtype):
+        return None
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+    except ImportError:
+        _fused_ok[key] = False
+        return None
+    if _FUSED_BACKENDS is None:
+        _FUSED_BACKENDS = [SDPBackend.EFFICIENT_ATTENTION, SDPBackend.FLASH_ATTENTION]
+    try:
+        with sdpa_kernel(_FUSED_BACKENDS):
+            out = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+    except RuntimeError:
+        # no fused kernel for these inputs (raised before any launch)
+        _fused_ok[key] = False
+        return None
+    _fused_ok[key] = True
+    return out
+
+
 class MultiHeadAttention(torch.nn.Module):
     """Causal multi-head attention with QK-norm and RoPE (attention.py:67-150).
 
@@ -220,11 +255,13 @@ class MultiHeadAttention(torch.nn.Module):
         if rotary is not None:
             cos, sin = rotary(q, seq_dim=2)
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
-        out = _CausalAttention.apply(
-            q.reshape(B * H, L, K).contiguous(), k.reshape(B * H, L, K).contiguous(),
-            v.reshape(B * H, L, K).contiguous(), self.head_dim ** 0.5,
-        )  # (B*H, L, K)
-        joined = out.view(B, H, L, K).permute(0, 2, 1, 3).reshape(B, L, H * K)
+        out = _fused_causal_attention(q, k, v) if q.is_cuda else None  # (B, H, L, K)
+        if out is None:
+            out = _CausalAttention.apply(
+                q.reshape(B * H, L, K).contiguous(), k.reshape(B * H, L, K).contiguous(),
+                v.reshape(B * H, L, K).contiguous(), self.head_dim ** 0.5,
+            ).view(B, H, L, K)
+        joined = out.permute(0, 2, 1, 3).reshape(B, L, H * K)
         return joined @ self.w_o_HKD.reshape(H * K, self.dim)  # (B, L, D)
 
 

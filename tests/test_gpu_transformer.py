@@ -98,3 +98,33 @@ def test_training_steps_reduce_loss_and_move_router_bias():
     assert all(torch.isfinite(torch.tensor(losses)))
     assert losses[-1] < losses[0], losses
     assert any(not torch.equal(b0, blk.moe.router.expert_bias_E) for b0, blk in zip(bias0, model.blocks))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 48, 4, 16), (1, 256, 2, 64)], ids=["L48_K16", "L256_K64"])
+def test_attention_matches_materialised_fp64(dtype, shape):
+    """MultiHeadAttention on the GPU (torch's fused causal kernel where it takes the
+    inputs) against the materialised attention of attention.py:136-141 in fp64."""
+    from abacus_amd import transformer as tr
+    B, L, H, K = shape
+    torch.manual_seed(6)
+    attn = tr.MultiHeadAttention(H * K, H, K)
+    rot = tr.Rotary(K)
+    x = torch.randn(B, L, H * K)
+
+    def run(mod, xx, rotary):
+        xx = xx.clone().requires_grad_()
+        out = mod(xx, rotary)
+        out.backward(torch.cos(torch.arange(out.numel(), dtype=out.dtype, device=out.device)).view_as(out))
+        grads = [xx.grad] + [p.grad for p in mod.parameters()]
+        return out.detach().double().cpu(), [g.detach().double().cpu() for g in grads]
+
+    got, got_g = run(copy.deepcopy(attn).to(dtype).cuda(), x.to(dtype).cuda(), copy.deepcopy(rot).to(dtype).cuda())
+    ref, ref_g = run(copy.deepcopy(attn).to(dtype), x.to(dtype), copy.deepcopy(rot).to(dtype))
+    tru, tru_g = run(copy.deepcopy(attn).double(), x.double(), copy.deepcopy(rot).double())
+    rtol = RTOL[dtype]
+    assert _rel(got, tru) <= max(2 * _rel(ref, tru), rtol)
+    for g, r, t in zip(got_g, ref_g, tru_g):
+        assert _rel(g, t) <= max(2 * _rel(r, t), rtol)
+    if dtype == torch.bfloat16 and K == 64:
+        assert tr._fused_ok.get((torch.bfloat16, 64)) is True, "fused attention did not run"
