@@ -79,6 +79,9 @@ struct GemmArgs {
   // split_parts <= 1: every tile runs whole.
   int split_from, split_parts, split_cus;
   float* split_ws;
+  // Pipelined kernel, row-grouped kinds: nonzero when expert remainders of at
+  // most THIN rows go to thin tiles (else every row tile is a full one).
+  int thin;
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -498,6 +501,22 @@ constexpr int TILE_CHUNKS = TILE_BYTES / 16;
 constexpr int DMA_PER_OPERAND = TILE_CHUNKS / NT;   // 16-byte chunks per thread per operand tile
 constexpr int LOADS_PER_TILE = 2 * DMA_PER_OPERAND; // DMA instructions per thread per k-tile
 
+// Row-grouped kinds cut each expert's rows into BM-row tiles; a remainder of
+// at most THIN rows goes to a thin tile of THIN rows (same 256 columns, same
+// MFMAs and k order, so the same results) instead of a mostly empty full one.
+constexpr int THIN = 128;
+template <int BMT>
+struct Geo {
+  static_assert(BMT == BM || BMT == THIN, "full or thin tiles");
+  static constexpr int WTM = BMT / WAVES_M, FM = WTM / 32;
+  static constexpr int A_BYTES = BMT * BK * 2;                 // A operand tile
+  static constexpr int STAGE = A_BYTES + TILE_BYTES;           // A + B
+  static constexpr int DMA_A = A_BYTES / 16 / NT, DMA_B = DMA_PER_OPERAND;
+  static constexpr int LOADS = DMA_A + DMA_B;                  // DMA instructions per thread per k-tile
+  static constexpr int LDS = STAGES * STAGE > BMT * LDC * 2 ? STAGES * STAGE : BMT * LDC * 2;
+};
+static_assert(Geo<BM>::LDS == LDS_BYTES && Geo<THIN>::LDS <= LDS_BYTES, "full tiles size the LDS");
+
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -562,17 +581,17 @@ __device__ inline float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.0f 
 // source pointers once and issue() adds the k0 step (kc: k0 elements, mc:
 // k0 rows) -- one 64-bit add per DMA.  Chunks whose k lies beyond k_lim
 // (a ragged segment's tail) read the zero page instead.
-template <bool MC>
+template <bool MC, int N = DMA_PER_OPERAND>
 struct DmaStream {
-  const uint16_t* base[DMA_PER_OPERAND];
-  int koff[DMA_PER_OPERAND];   // k of the chunk relative to k0
+  const uint16_t* base[N];
+  int koff[N];   // k of the chunk relative to k0
   int64_t ld;
 
   __device__ inline void setup(const uint16_t* b0, const uint16_t* b1, int64_t ld_, int r0, int r_lim, int wave,
                                int lane) {
     ld = ld_;
 #pragma unroll
-    for (int i = 0; i < DMA_PER_OPERAND; ++i) {
+    for (int i = 0; i < N; ++i) {
       const int p = (i * NWAVES + wave) * 64 + lane;
       if (!MC) {
         const int row = p / CPR;
@@ -652,10 +671,40 @@ __device__ inline int xcd_logical(int b, int G) { return (b & 7) * (G >> 3) + (b
 // tiles) are numbered in the same GM x GN groups, the last group of rows
 // possibly short.  Each XCD takes an equal, contiguous share of them, so no
 // XCD is left with the padding of the host's upper bound.
+// Row tiles of BMT rows for an expert with `rows` routed rows: rows / BM full
+// tiles, then the remainder in one more full tile when it exceeds THIN rows,
+// else (when nonzero) in one thin tile.
+template <int BMT>
+__host__ __device__ inline int expert_row_tiles(int rows, int thin) {
+  const int rem = rows % BM;
+  if (!thin) return BMT == BM ? (rows + BM - 1) / BM : 0;
+  return BMT == BM ? rows / BM + (rem > THIN ? 1 : 0) : (rem > 0 && rem <= THIN ? 1 : 0);
+}
+
+template <int BMT>
 __device__ inline int count_row_tiles(const GemmArgs& g) {
   int n = 0;
-  for (int i = 0; i < g.E; ++i) n += (g.offsets[i + 1] - g.offsets[i] + BM - 1) / BM;
+  for (int i = 0; i < g.E; ++i) n += expert_row_tiles<BMT>(g.offsets[i + 1] - g.offsets[i], g.thin);
   return n;
+}
+
+// Row tile mt (of the BMT-row tiles, experts in order) -> its expert and its
+// rows row0 .. row_end-1 of that expert's range.  False: no such tile.
+template <int BMT>
+__device__ inline bool find_row_tile(const GemmArgs& g, int mt, int& e, int& row0, int& row_end) {
+  int acc = 0;
+  for (int i = 0; i < g.E; ++i) {
+    const int a = g.offsets[i], b = g.offsets[i + 1];
+    const int nt = expert_row_tiles<BMT>(b - a, g.thin);
+    if (mt < acc + nt) {
+      e = i;
+      row0 = BMT == BM ? a + (mt - acc) * BM : a + (b - a) / BM * BM;
+      row_end = b;
+      return true;
+    }
+    acc += nt;
+  }
+  return false;
 }
 
 __device__ inline void row_tile(int r, int mt_real, int NTp, int& mt, int& nt) {
@@ -719,13 +768,18 @@ __device__ inline TileId tile_of_logical(int L, int MTp, int NTp) {
   return t;
 }
 
-// One 256 x 256 output tile of a GEMM kind: block b of the kind's G blocks
-// (G a multiple of 8, so b % 8 is still the XCD the block runs on when a
-// launch runs several kinds back to back).  lds: the work-group's LDS_BYTES.
-template <int KIND>
+// One BMT x 256 output tile of a GEMM kind (BMT = BM, or THIN for the thin
+// row tiles of row-grouped kinds): block b of the kind's G blocks (G a
+// multiple of 8, so b % 8 is still the XCD the block runs on when a launch
+// runs several kinds back to back).  lds: the work-group's LDS_BYTES.
+template <int KIND, int BMT = BM>
 __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& g, int b, int G, char* lds) {
   using KT = KindTraits<KIND>;
   using Op = MfmaOp<uint16_t, 32>;
+  using GE = Geo<BMT>;
+  static_assert(!KT::WGRAD || BMT == BM, "weight gradients have full tiles only");
+  constexpr int FM = GE::FM, WTM = GE::WTM, STAGE_BYTES = GE::STAGE, A_BYTES = GE::A_BYTES;
+  constexpr int LOADS_PER_TILE = GE::LOADS, DMA_A = GE::DMA_A;
   static_assert(!KindTraits<KIND>::DUAL_B || FN % 2 == 0, "dual-B pairs gate/up fragments");
   constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
 
@@ -739,7 +793,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   int part = -1, slot = 0;  // slice of a split tail tile, its workspace slot
   TileId tl;
   if (!KT::WGRAD) {
-    const int mt_real = count_row_tiles(g);
+    const int mt_real = count_row_tiles<BMT>(g);
     const int total = mt_real * g.tiles_n;
     int r;
     if (!block_to_row_tile(g, b, total, r, part)) return;
@@ -752,20 +806,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   n0 = tl.nt * BNH;
   if (n0 >= g.Ndim) return;
   if (!KT::WGRAD) {
-    int acc_tiles = 0;
-    const int bx = tl.mt;
-    for (int i = 0; i < g.E; ++i) {
-      const int a = g.offsets[i], b = g.offsets[i + 1];
-      const int nt = (b - a + BM - 1) / BM;
-      if (bx < acc_tiles + nt) {
-        e = i;
-        row0 = a + (bx - acc_tiles) * BM;
-        row_end = b;
-        break;
-      }
-      acc_tiles += nt;
-    }
-    if (e < 0) return;
+    if (!find_row_tile<BMT>(g, tl.mt, e, row0, row_end)) return;
     k_len = g.Kdim;
   } else {
     e = tl.e;
@@ -791,7 +832,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // a slice of a split tile runs k-tiles kbase .. kbase + ktiles - 1
   int kbase = 0, ktiles = ktiles_all;
   if (part >= 0) {
-    const int S = split_slices(g, count_row_tiles(g) * g.tiles_n % g.split_cus);
+    const int S = split_slices(g, count_row_tiles<BMT>(g) * g.tiles_n % g.split_cus);
     const int per = (ktiles_all + S - 1) / S;
     kbase = part * per;
     ktiles = max(0, min(per, ktiles_all - kbase));
@@ -800,7 +841,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 
   // wave index as a scalar so the DMA destinations are computed in SGPRs
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  DmaStream<KT::A_MC> sa;
+  DmaStream<KT::A_MC, DMA_A> sa;
   DmaStream<KT::B_NC> sb;
   int half_set = 0;
   sa.setup(A0, nullptr, g.lda, row0, a_lim, wave, lane);
@@ -822,8 +863,8 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     dma_k0 = (kt - half * ktiles_half) * BK;
   };
   auto dma = [&](int n) __attribute__((always_inline)) {
-    if (n < DMA_PER_OPERAND) sa.template issue_one<KT::WGRAD>(n, dma_stage, wave_u, dma_k0, k_len);
-    else sb.template issue_one<KT::WGRAD>(n - DMA_PER_OPERAND, dma_stage + TILE_BYTES, wave_u, dma_k0, k_len);
+    if (n < DMA_A) sa.template issue_one<KT::WGRAD>(n, dma_stage, wave_u, dma_k0, k_len);
+    else sb.template issue_one<KT::WGRAD>(n - DMA_A, dma_stage + A_BYTES, wave_u, dma_k0, k_len);
   };
 
   Op::Acc acc[FM][FN];
@@ -851,7 +892,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   constexpr int NFRAG = FM + FN;
   auto read_frag = [&](const char* st, int t, int slot, int f) __attribute__((always_inline)) {
     const char* At = st;
-    const char* Bt = st + TILE_BYTES;
+    const char* Bt = st + A_BYTES;
     if (f == 0 || f > FN) {
       const int i = f == 0 ? 0 : f - FN;
       af[slot][i] = KT::A_MC ? frag_mc(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
@@ -863,19 +904,24 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 
   // One k-step: the FM x FN MFMAs on fragment slot `slot`.  Fragment read f
   // of the next step (from stage rd_st, step rd_t, into slot rd_slot) follows
-  // MFMA f; when `with_dma`, DMA instruction m follows MFMA m.  Each group is
+  // MFMA f; when `with_dma`, the k-tile's DMA instructions follow the MFMAs
+  // evenly (one each for full tiles, one or two for thin ones).  Each group is
   // fenced with sched_barrier so the interleave survives scheduling: with one
   // wave per SIMD, nothing else keeps the matrix core busy while this wave
   // waits on LDS or issues loads.
   auto kstep = [&](int slot, bool with_read, const char* rd_st, int rd_t, int rd_slot, bool with_dma) __attribute__((always_inline)) {
-    static_assert(FM * FN >= NFRAG && FM * FN >= LOADS_PER_TILE, "one read and one DMA per MFMA at most");
+    constexpr int MF = FM * FN;
+    static_assert(MF >= NFRAG, "one fragment read per MFMA at most");
 #pragma unroll
-    for (int m = 0; m < FM * FN; ++m) {
+    for (int m = 0; m < MF; ++m) {
       // operands swapped: the fragment is C^T, so each lane ends up holding
       // runs of 4 consecutive columns of one row (see the epilogue)
       Op::run(acc[m / FN][m % FN], bfr[slot][m % FN], af[slot][m / FN]);
       if (with_read && m < NFRAG) read_frag(rd_st, rd_t, rd_slot, m);
-      if (with_dma && m < LOADS_PER_TILE) dma(m);
+      if (with_dma) {
+#pragma unroll
+        for (int n = m * LOADS_PER_TILE / MF; n < (m + 1) * LOADS_PER_TILE / MF; ++n) dma(n);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -960,7 +1006,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // the C tile is staged, so HBM latency is paid about once per tile.
   constexpr int VEC = 8;
   constexpr int CV = BNH / VEC;
-  constexpr int NV = BM * CV / NT;  // vectors per thread
+  constexpr int NV = BMT * CV / NT;  // vectors per thread
   constexpr int BATCH = 8;
   constexpr int NBATCH = NV / BATCH;
   static_assert(NV % BATCH == 0, "whole batches");
@@ -1064,16 +1110,23 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
   gemm_tile<KIND>(g, blockIdx.x, gridDim.x, lds);
 }
 
-// Two independent GEMMs in one launch: blocks [0, ga_blocks) run kind KA's
-// tiles, the rest kind KB's.  Blocks are dispatched in index order, so when KA
-// has the long tiles (a data gradient over the full reduction) and KB the
-// short ones (a weight gradient over one expert's rows), KB's tiles fill the
-// CUs that KA's last partial round of tiles would leave idle.
-template <int KA, int KB>
-__global__ __launch_bounds__(NT, 1) void gemm_bf16_pair_kernel(GemmArgs ga, GemmArgs gb, int ga_blocks) {
+// A row-grouped kind's full tiles, then its thin tiles, then (KW >= 0) a
+// weight gradient's tiles, in one launch: blocks [0, n1), [n1, n1 + n2), and
+// the rest (n1 and n2 multiples of 8).  Blocks are dispatched in index order,
+// so the long tiles go first and the shorter ones fill the CUs that the long
+// tiles' last partial round would leave idle.
+template <int KR, int KW>
+__global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, GemmArgs g2, GemmArgs g3, int n1,
+                                                               int n2) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
-  if ((int)blockIdx.x < ga_blocks) gemm_tile<KA>(ga, blockIdx.x, ga_blocks, lds);
-  else gemm_tile<KB>(gb, (int)blockIdx.x - ga_blocks, (int)gridDim.x - ga_blocks, lds);
+  const int b = blockIdx.x;
+  if (b < n1) {
+    gemm_tile<KR, BM>(g1, b, n1, lds);
+  } else if (b < n1 + n2) {
+    gemm_tile<KR, THIN>(g2, b - n1, n2, lds);
+  } else {
+    if constexpr (KW >= 0) gemm_tile<KW, BM>(g3, b - n1 - n2, (int)gridDim.x - n1 - n2, lds);
+  }
 }
 
 // Adds the slices of each split tail tile in slice order and writes the tile
@@ -1083,7 +1136,7 @@ template <int KIND>
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   using KT = KindTraits<KIND>;
   static_assert(!KT::WGRAD && !KT::DUAL_B && KIND != kDownDgrad, "plain-store epilogues only");
-  const int mt_real = count_row_tiles(g);
+  const int mt_real = count_row_tiles<BM>(g);
   const int total = mt_real * g.tiles_n;
   const int whole = total / g.split_cus * g.split_cus;
   const int S = split_slices(g, total - whole);
@@ -1092,17 +1145,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   row_tile(whole + (int)blockIdx.x, mt_real, g.tiles_n, tl.mt, tl.nt);
   const int n0 = tl.nt * BN;
   if (n0 >= g.Ndim) return;
-  int row0 = 0, row_end = 0, acc_tiles = 0;
-  for (int i = 0; i < g.E; ++i) {
-    const int a = g.offsets[i], b = g.offsets[i + 1];
-    const int nt = (b - a + BM - 1) / BM;
-    if (tl.mt < acc_tiles + nt) {
-      row0 = a + (tl.mt - acc_tiles) * BM;
-      row_end = b;
-      break;
-    }
-    acc_tiles += nt;
-  }
+  int e = 0, row0 = 0, row_end = 0;
+  if (!find_row_tile<BM>(g, tl.mt, e, row0, row_end)) return;
   const float* ws = g.split_ws + (int64_t)blockIdx.x * g.split_parts * (BM * BN);
   constexpr int CV = BN / 8;
   for (int v = threadIdx.x; v < BM * CV; v += 256) {
@@ -1173,15 +1217,52 @@ int64_t pipe_grid(GemmArgs& g, int R) {
   return (int64_t)(KT::WGRAD ? g.E : 1) * g.tiles_m * g.tiles_n;
 }
 
+// The thin row tiles of a row-grouped kind: at most one per expert, in the
+// same column tiles.  Returns the number of blocks, a multiple of 8.
 template <int KIND>
-int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
-  GemmArgs ga = g;
-  const int64_t total = pipe_grid<KIND>(ga, R);
-  if (total == 0) return 0;
-  ABACUS_CHECK_ARG(total < (1ll << 31), "%s: tile grid too large", name);
-  hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)total), dim3(pipe::NT), 0, s, ga);
+int64_t pipe_grid_thin(GemmArgs& g, int R) {
+  static_assert(!KindTraits<KIND>::WGRAD, "row-grouped kinds");
+  if (pipe_grid<KIND>(g, R) == 0) return 0;
+  g.tiles_m = pipe::round_up(g.E, pipe::GM);
+  g.split_parts = 0;  // thin tiles always run whole
+  return pipe::round_up(g.E * g.tiles_n, 8);
+}
+
+// One launch of a row-grouped kind KR (full tiles from g1, whose split-tail
+// fields may be set, then thin tiles) and, when KW >= 0, a weight gradient
+// (gw) after them.
+template <int KR, int KW>
+int launch_rows(const GemmArgs& g1, int R, const GemmArgs* gw, int64_t n1, bool thin, hipStream_t s,
+                const char* name) {
+  GemmArgs ga = g1, gt = g1, gc = gw ? *gw : g1;
+  ga.thin = gt.thin = thin ? 1 : 0;
+  const int64_t full = pipe_grid<KR>(ga, R);
+  if (n1 < 0) n1 = full;  // no split: one block per full tile of the upper bound
+  const int64_t n2 = thin ? pipe_grid_thin<KR>(gt, R) : 0;
+  const int64_t n3 = KW >= 0 ? pipe_grid<(KW >= 0 ? KW : KR)>(gc, R) : 0;
+  ABACUS_CHECK_ARG(n1 + n2 + n3 < (1ll << 31), "%s: tile grid too large", name);
+  if (n1 + n2 + n3 == 0) return 0;
+  hipLaunchKernelGGL((pipe::gemm_bf16_rows_kernel<KR, KW>), dim3((unsigned)(n1 + n2 + n3)), dim3(pipe::NT), 0, s, ga,
+                     gt, gc, (int)n1, (int)n2);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
+}
+
+template <int KIND>
+int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
+  if constexpr (!KindTraits<KIND>::WGRAD) {
+    // (the down projection's forward reduces over M: its tiles are long, and
+    // thin ones would end the launch on a partial round of them)
+    return launch_rows<KIND, -1>(g, R, nullptr, -1, KIND != kDownFwd, s, name);
+  } else {
+    GemmArgs ga = g;
+    const int64_t total = pipe_grid<KIND>(ga, R);
+    if (total == 0) return 0;
+    ABACUS_CHECK_ARG(total < (1ll << 31), "%s: tile grid too large", name);
+    hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)total), dim3(pipe::NT), 0, s, ga);
+    ABACUS_CHECK_LAUNCH(name);
+    return 0;
+  }
 }
 
 // CUs of the current device (one work-group of the pipelined kernel fits a
@@ -1233,25 +1314,20 @@ int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws
   ga.split_parts = kSplitParts;
   ga.split_cus = cu_count();
   ga.split_ws = ws;
-  const int64_t blocks = (int64_t)plan.whole_blocks + plan.slice_blocks;
-  hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
-  ABACUS_CHECK_LAUNCH(name);
+  if (launch_rows<KIND, -1>(ga, R, nullptr, (int64_t)plan.whole_blocks + plan.slice_blocks, false, s, name))
+    return 1;
+  ga.thin = 0;
   hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail_max), dim3(256), 0, s, ga);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
 
-// Kinds KA (the long tiles) and KB in one launch.
+// A data gradient (KA, row-grouped: the long tiles, then its thin ones) and a
+// weight gradient (KB) in one launch.
 template <int KA, int KB>
 int launch_pipe_pair(const GemmArgs& a, int Ra, const GemmArgs& b, int Rb, hipStream_t s, const char* name) {
-  GemmArgs ga = a, gb = b;
-  const int64_t na = pipe_grid<KA>(ga, Ra), nb = pipe_grid<KB>(gb, Rb);
-  ABACUS_CHECK_ARG(na + nb < (1ll << 31), "%s: tile grid too large", name);
-  if (na + nb == 0) return 0;
-  hipLaunchKernelGGL((pipe::gemm_bf16_pair_kernel<KA, KB>), dim3((unsigned)(na + nb)), dim3(pipe::NT), 0, s, ga, gb,
-                     (int)na);
-  ABACUS_CHECK_LAUNCH(name);
-  return 0;
+  (void)Rb;
+  return launch_rows<KA, KB>(a, Ra, &b, -1, true, s, name);
 }
 
 // bf16: the pipelined DMA kernel whenever every dimension it tiles is a
