@@ -160,3 +160,50 @@ def test_down_fwd_split_tail():
         want = h[a:b].float() @ w_down[e].float()
         err = float((split1[a:b].float() - want).norm() / want.norm())
         assert err < 1e-2, f"expert {e}: relative error {err:.3g}"
+
+
+def test_row_tiles_every_remainder_class():
+    """Row-grouped products for experts whose last rows fill a full tile, spill into one
+    (remainder > 128 rows) or fit a thin 128-row tile (1..128 rows), plus empty and
+    sub-128-row experts: every row written, each expert's rows equal to its fp64 product."""
+    counts, D, M = [256, 257, 383, 384, 385, 511, 512, 1, 128, 129, 0, 130], 256, 256
+    o = _operands(counts, D, M, torch.bfloat16, seed=21)
+    E, R = o["E"], o["R"]
+    s = _lib.stream_of(torch.device("cuda"))
+    dev = "cuda"
+    nan = lambda *shape: torch.full(shape, float("nan"), dtype=torch.bfloat16, device=dev)
+    G, U, H, Y = nan(R, M), nan(R, M), nan(R, M), nan(R, D)
+    dG, dU, dX = nan(R, M), nan(R, M), nan(R, D)
+    call("abacus_moe_gateup_fwd", ptr(o["xp"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["offsets"]), R, D, M, E, 1,
+         ptr(G), ptr(U), ptr(H), s)
+    call("abacus_moe_down_fwd", ptr(o["h"]), ptr(o["w_down"]), ptr(o["offsets"]), R, M, D, E, 1, ptr(Y), None, 0, s)
+    call("abacus_moe_down_bwd_dgrad", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]),
+         ptr(o["offsets"]), R, M, D, E, 1, ptr(dG), ptr(dU), s)
+    call("abacus_moe_gateup_bwd_dgrad", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]),
+         ptr(o["offsets"]), R, D, M, E, 1, ptr(dX), s)
+    torch.cuda.synchronize()
+    for name, t in (("G", G), ("U", U), ("H", H), ("Y", Y), ("dG", dG), ("dU", dU), ("dX", dX)):
+        assert not torch.isnan(t).any(), f"{name}: rows left unwritten"
+    f = lambda t: t.double().cpu()
+    off = o["offsets"].tolist()
+
+    def close(got, want, what, tol=1e-2):
+        err = float((f(got) - want).norm() / max(want.norm().item(), 1e-30))
+        assert err < tol, f"{what}: relative error {err:.3g}"
+
+    for e in range(E):
+        a, b = off[e], off[e + 1]
+        if a == b:
+            continue
+        close(G[a:b], f(o["xp"][a:b]) @ f(o["w_gate"][e]), f"G expert {e}")
+        close(U[a:b], f(o["xp"][a:b]) @ f(o["w_up"][e]), f"U expert {e}")
+        g, u = f(G[a:b]), f(U[a:b])
+        close(H[a:b], g * torch.sigmoid(g) * u, f"H expert {e}")
+        close(Y[a:b], f(o["h"][a:b]) @ f(o["w_down"][e]), f"Y expert {e}")
+        dh = f(o["dy"][a:b]) @ f(o["w_down"][e]).T
+        gg, uu = f(o["gate"][a:b]), f(o["up"][a:b])
+        sg = torch.sigmoid(gg)
+        close(dG[a:b], dh * uu * sg * (1 + gg * (1 - sg)), f"dG expert {e}", 2e-2)
+        close(dU[a:b], dh * gg * sg, f"dU expert {e}", 2e-2)
+        close(dX[a:b], f(o["dgate"][a:b]) @ f(o["w_gate"][e]).T + f(o["dup"][a:b]) @ f(o["w_up"][e]).T,
+              f"dX expert {e}")
