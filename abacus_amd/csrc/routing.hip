@@ -579,64 +579,157 @@ __global__ __launch_bounds__(256) void router_wgrad_partial_kernel(const T* __re
   }
 }
 
-// dW_DE partials for E <= EMAX: each thread owns 4 consecutive columns and
-// keeps their E accumulators in registers.  A token's K (expert, dlogit)
-// pairs are the same for every thread of the block (scalar loads); they are
-// expanded to a dense coefficient row, so the accumulator index is a
-// compile-time constant.  Tokens are added in order within a chunk.
+// dW_DE partials for E <= EMAX.  The block first expands its chunk's
+// (expert, dlogit) pairs into a dense (token, expert) coefficient table in
+// LDS, one thread per token (adding in slot order).  Each lane of a wave owns
+// 16 bytes of consecutive columns (8 bf16 or 4 fp32) and keeps their E
+// accumulators in registers; the block's 4 waves share those columns and
+// take consecutive quarters of the chunk's tokens (added in order, 8 token
+// rows of loads in flight), and their sums are added in wave order through
+// LDS.
+constexpr int kWgradChunkMax = 256;  // tokens per chunk (the coefficient table)
 template <typename T, int EMAX>
-__global__ __launch_bounds__(256) void router_wgrad_partial_reg_kernel(const T* __restrict__ x,
+__global__ __launch_bounds__(256, 1) void router_wgrad_partial_reg_kernel(const T* __restrict__ x,
                                                                        const float* __restrict__ dlogit,
                                                                        const int32_t* __restrict__ idx, int T_, int D,
                                                                        int E, int K, int chunk,
                                                                        float* __restrict__ partial) {
-  constexpr int CPT = 4;
-  const int d0 = (blockIdx.x * 256 + threadIdx.x) * CPT;
+  constexpr int CPT = 16 / (int)sizeof(T);
+  constexpr int EG = 4;  // experts per round of the wave-sum exchange
+  static_assert(EMAX % EG == 0, "whole rounds");
+  __shared__ float coef_s[kWgradChunkMax * EMAX];
+  __shared__ float4 red_s[3][EG][CPT / 4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = blockIdx.y;
   const int ta = c * chunk;
-  const int tb = min(T_, ta + chunk);
+  const int n = max(0, min(T_, ta + chunk) - ta);
+  for (int t = threadIdx.x; t < n; t += blockDim.x) {
+    float row[EMAX];
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) row[e] = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int ek = idx[(int64_t)(ta + t) * K + k];
+      const float wk = dlogit[(int64_t)(ta + t) * K + k];
+#pragma unroll
+      for (int e = 0; e < EMAX; ++e) row[e] = ek == e ? row[e] + wk : row[e];
+    }
+#pragma unroll
+    for (int e = 0; e < EMAX; ++e) coef_s[t * EMAX + e] = row[e];
+  }
+  __syncthreads();
+  const int d0 = (blockIdx.x * 64 + lane) * CPT;
+  const bool active = d0 < D;
+  const int q = (n + 3) / 4, t0 = min(n, w * q), t1 = min(n, t0 + q);
   float acc[EMAX][CPT];
 #pragma unroll
   for (int e = 0; e < EMAX; ++e)
 #pragma unroll
     for (int j = 0; j < CPT; ++j) acc[e][j] = 0.f;
-  if (d0 < D) {
-#pragma unroll 4
-    for (int t = ta; t < tb; ++t) {
+  if (active) {
+    const T* xp = x + (int64_t)ta * D + d0;
+#pragma unroll 8
+    for (int t = t0; t < t1; ++t) {
+      const uint4 v = *reinterpret_cast<const uint4*>(xp + (int64_t)t * D);
       float xv[CPT];
       if constexpr (sizeof(T) == 2) {
-        const uint2 w = *reinterpret_cast<const uint2*>(x + (int64_t)t * D + d0);
-        xv[0] = bits_f32(w.x << 16);
-        xv[1] = bits_f32(w.x & 0xffff0000u);
-        xv[2] = bits_f32(w.y << 16);
-        xv[3] = bits_f32(w.y & 0xffff0000u);
+        const uint32_t ww[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xv[2 * i] = bits_f32(ww[i] << 16);
+          xv[2 * i + 1] = bits_f32(ww[i] & 0xffff0000u);
+        }
       } else {
-        const float4 w = *reinterpret_cast<const float4*>(x + (int64_t)t * D + d0);
-        xv[0] = w.x;
-        xv[1] = w.y;
-        xv[2] = w.z;
-        xv[3] = w.w;
-      }
-      float coef[EMAX];
-#pragma unroll
-      for (int e = 0; e < EMAX; ++e) coef[e] = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const int ek = idx[(int64_t)t * K + k];
-        const float wk = dlogit[(int64_t)t * K + k];
-#pragma unroll
-        for (int e = 0; e < EMAX; ++e) coef[e] = ek == e ? coef[e] + wk : coef[e];
+        xv[0] = bits_f32(v.x);
+        xv[1] = bits_f32(v.y);
+        xv[2] = bits_f32(v.z);
+        xv[3] = bits_f32(v.w);
       }
 #pragma unroll
-      for (int e = 0; e < EMAX; ++e)
+      for (int e = 0; e < EMAX; ++e) {
+        const float cf = coef_s[t * EMAX + e];
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) acc[e][j] += xv[j] * coef[e];
+        for (int j = 0; j < CPT; ++j) acc[e][j] += xv[j] * cf;
+      }
     }
+  }
+  // wave sums, added in wave order, EG experts per round
 #pragma unroll
-    for (int e = 0; e < EMAX; ++e)
-      if (e < E) {
+  for (int e0 = 0; e0 < EMAX; e0 += EG) {
+    if (e0 >= E) continue;  // E is uniform: every thread skips the same rounds
+    if (w > 0) {
 #pragma unroll
-        for (int j = 0; j < CPT; ++j) partial[((int64_t)c * E + e) * D + d0 + j] = acc[e][j];
+      for (int g = 0; g < EG; ++g)
+#pragma unroll
+        for (int j = 0; j < CPT; j += 4)
+          red_s[w - 1][g][j / 4][lane] =
+              make_float4(acc[e0 + g][j], acc[e0 + g][j + 1], acc[e0 + g][j + 2], acc[e0 + g][j + 3]);
+    }
+    __syncthreads();
+    if (w == 0 && active) {
+#pragma unroll
+      for (int g = 0; g < EG; ++g) {
+        if (e0 + g >= E) continue;
+        float* out = partial + ((int64_t)c * E + e0 + g) * D + d0;
+#pragma unroll
+        for (int j = 0; j < CPT; j += 4) {
+          float4 r = make_float4(acc[e0 + g][j], acc[e0 + g][j + 1], acc[e0 + g][j + 2], acc[e0 + g][j + 3]);
+#pragma unroll
+          for (int o = 0; o < 3; ++o) {
+            const float4 u = red_s[o][g][j / 4][lane];
+            r.x += u.x;
+            r.y += u.y;
+            r.z += u.z;
+            r.w += u.w;
+          }
+          *reinterpret_cast<float4*>(out + j) = r;
+        }
       }
+    }
+    __syncthreads();
+  }
+}
+
+// dW_DE from the chunk partials [chunk][e][d] when E * D is a multiple of 4:
+// a block takes 64 float4 runs of the (e, d) order; its 4 waves add chunks
+// c = w, w + 4, ... in order, then wave 0 adds the 4 sums in wave order.
+template <typename T>
+__global__ __launch_bounds__(256) void router_wgrad_reduce4_kernel(const float* __restrict__ partial, int nchunks,
+                                                                   int D, int E, T* __restrict__ dw) {
+  __shared__ float4 part_s[4][64];
+  const int v_lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t nv = (int64_t)E * D / 4;
+  const int64_t v = (int64_t)blockIdx.x * 64 + v_lane;
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (v < nv) {
+    const float4* p = reinterpret_cast<const float4*>(partial) + v;
+#pragma unroll 8
+    for (int c = w; c < nchunks; c += 4) {
+      const float4 q = p[(int64_t)c * nv];
+      sum.x += q.x;
+      sum.y += q.y;
+      sum.z += q.z;
+      sum.w += q.w;
+    }
+  }
+  part_s[w][v_lane] = sum;
+  __syncthreads();
+  if (w == 0 && v < nv) {
+    float4 r = part_s[0][v_lane];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      const float4 o = part_s[q][v_lane];
+      r.x += o.x;
+      r.y += o.y;
+      r.z += o.z;
+      r.w += o.w;
+    }
+    const float rv[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t f = v * 4 + j;
+      const int e = (int)(f / D), d = (int)(f % D);
+      dw[(int64_t)d * E + e] = from_f32<T>(rv[j]);
+    }
   }
 }
 
@@ -868,26 +961,37 @@ int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, con
   return 0;
 }
 
-// The register path (4 columns per thread, E <= 16) needs D % 4 == 0; the
-// column path takes any D and E.
-static bool router_wgrad_reg_path(int64_t D, int64_t E) { return E <= 16 && D % 4 == 0; }
+// The register path (16 bytes of columns per lane, 64 lanes' columns per
+// block, E <= 16) needs D to be a whole number of 16-byte runs; the column
+// path takes any D and E.
+static int wgrad_cpt(int dtype) { return dtype == kBF16 ? 8 : 4; }
+static bool router_wgrad_reg_path(int64_t D, int64_t E, int dtype) { return E <= 16 && D % wgrad_cpt(dtype) == 0; }
 
-static void router_wgrad_plan(int64_t T, int64_t D, bool reg, int* chunk, int* nchunks) {
-  const int64_t cols_per_block = reg ? 1024 : 256;
+// Token chunks of the partial pass: enough blocks to fill the GPU (~512),
+// partials of at most half the bytes of x, at most kWgradChunkMax tokens.
+static void router_wgrad_plan(int64_t T, int64_t D, int64_t E, int dtype, bool reg, int* chunk, int* nchunks) {
+  const int64_t cols_per_block = reg ? 64 * wgrad_cpt(dtype) : 256;
   const int64_t dblocks = (D + cols_per_block - 1) / cols_per_block;
-  int64_t want = std::max<int64_t>(1, 512 / dblocks);
-  int64_t nc = std::min<int64_t>(want, std::max<int64_t>(1, (T + 63) / 64));
+  const int64_t elem = dtype == kBF16 ? 2 : 4;
+  int64_t nc = std::max<int64_t>(1, 512 / dblocks);
+  nc = std::min<int64_t>(nc, std::max<int64_t>(1, T * elem / (8 * E)));
+  nc = std::min<int64_t>(nc, std::max<int64_t>(1, T));
   int64_t ch = (T + nc - 1) / nc;
   if (ch < 1) ch = 1;
+  if (reg && ch > kWgradChunkMax) ch = kWgradChunkMax;
   *chunk = (int)ch;
-  *nchunks = (int)((T + ch - 1) / ch);
-  if (*nchunks < 1) *nchunks = 1;
+  *nchunks = (int)std::max<int64_t>(1, (T + ch - 1) / ch);
 }
 
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E) {
-  int chunk, nchunks;
-  router_wgrad_plan(T, D, router_wgrad_reg_path(D, E), &chunk, &nchunks);
-  return (int64_t)nchunks * E * D * 4;
+  // sized for the larger of the two dtypes' plans
+  int64_t best = 0;
+  for (int dtype : {kF32, kBF16}) {
+    int chunk, nchunks;
+    router_wgrad_plan(T, D, E, dtype, router_wgrad_reg_path(D, E, dtype), &chunk, &nchunks);
+    best = std::max<int64_t>(best, (int64_t)nchunks * E * D * 4);
+  }
+  return best;
 }
 
 int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
@@ -896,13 +1000,13 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
   ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
   ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
   hipStream_t s = (hipStream_t)stream;
-  const bool reg = router_wgrad_reg_path(D, E);
+  const bool reg = router_wgrad_reg_path(D, E, dtype);
   int chunk, nchunks;
-  router_wgrad_plan(T, D, reg, &chunk, &nchunks);
-  const int g2 = (int)((D * E + 255) / 256);
+  router_wgrad_plan(T, D, E, dtype, reg, &chunk, &nchunks);
   // With T == 0 the partial kernel visits no tokens and writes zero partials.
   if (reg) {
-    const dim3 g1((unsigned)((D + 1023) / 1024), (unsigned)nchunks);
+    const int cols = 64 * wgrad_cpt(dtype);
+    const dim3 g1((unsigned)((D + cols - 1) / cols), (unsigned)nchunks);
 #define ABACUS_WGRAD_REG(TT, EM)                                                                               \
   hipLaunchKernelGGL((router_wgrad_partial_reg_kernel<TT, EM>), g1, dim3(256), 0, s, (const TT*)x_TD, dlogit_TK, \
                      idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws)
@@ -924,12 +1028,23 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
                        idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
   }
   ABACUS_CHECK_LAUNCH("router_wgrad_partial");
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(router_wgrad_reduce_kernel<uint16_t>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks,
-                       (int)D, (int)E, (uint16_t*)dw_DE);
-  else
-    hipLaunchKernelGGL(router_wgrad_reduce_kernel<float>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks, (int)D,
-                       (int)E, (float*)dw_DE);
+  if ((E * D) % 4 == 0) {
+    const unsigned g2 = (unsigned)((E * D / 4 + 63) / 64);
+    if (dtype == kBF16)
+      hipLaunchKernelGGL(router_wgrad_reduce4_kernel<uint16_t>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks,
+                         (int)D, (int)E, (uint16_t*)dw_DE);
+    else
+      hipLaunchKernelGGL(router_wgrad_reduce4_kernel<float>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks, (int)D,
+                         (int)E, (float*)dw_DE);
+  } else {
+    const int g2 = (int)((D * E + 255) / 256);
+    if (dtype == kBF16)
+      hipLaunchKernelGGL(router_wgrad_reduce_kernel<uint16_t>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks,
+                         (int)D, (int)E, (uint16_t*)dw_DE);
+    else
+      hipLaunchKernelGGL(router_wgrad_reduce_kernel<float>, dim3(g2), dim3(256), 0, s, partial_ws, nchunks, (int)D,
+                         (int)E, (float*)dw_DE);
+  }
   ABACUS_CHECK_LAUNCH("router_wgrad_reduce");
   return 0;
 }
