@@ -27,6 +27,7 @@ from __future__ import annotations
 
 import torch
 
+from . import _lib
 from .moe import MoE, MoEExpertParallel, _rank_and_world_size
 
 __all__ = [
@@ -102,8 +103,59 @@ def apply_rotary_pos_emb(q, k, cos, sin):
     return (q * cos) + (rotate_half(q) * sin), (k * cos) + (rotate_half(k) * sin)
 
 
+def _fused_norm_ok(x: torch.Tensor, gamma: torch.Tensor) -> bool:
+    """The HIP RMSNorm takes x: GPU, fp32/bf16, gamma of the same dtype, and rows whose
+    16-byte vectors split evenly over a power-of-two number of lanes (at most 8 each)."""
+    if not (x.is_cuda and x.dtype in (torch.float32, torch.bfloat16) and gamma.dtype == x.dtype):
+        return False
+    D = x.shape[-1]
+    epv = 8 if x.dtype == torch.bfloat16 else 4
+    if D % epv:
+        return False
+    nvec, lpr = D // epv, 64
+    while lpr > 1 and nvec % lpr:
+        lpr //= 2
+    return nvec // lpr in (1, 2, 4, 8)
+
+
+class _RMSNormFunction(torch.autograd.Function):
+    """gamma * x / sqrt(mean(x^2) + eps) as one HIP kernel each way (fp32 inside,
+    one rounding per output; dgamma reduced in a fixed order)."""
+
+    @staticmethod
+    def forward(ctx, x, gamma, eps: float):
+        D = x.shape[-1]
+        xc = x.contiguous()
+        rows = xc.numel() // D
+        y = torch.empty_like(xc)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+        _lib.call("abacus_rmsnorm_fwd", _lib.ptr(xc), _lib.ptr(gamma.contiguous()), rows, D, eps,
+                  _lib.dtype_code(x.dtype), _lib.ptr(y), _lib.ptr(rstd), _lib.stream_of(x.device))
+        ctx.save_for_backward(xc, gamma, rstd)
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        xc, gamma, rstd = ctx.saved_tensors
+        D = xc.shape[-1]
+        rows = xc.numel() // D
+        dyc = dy.contiguous()
+        dx = torch.empty_like(xc)
+        dgamma = torch.empty_like(gamma)
+        nbytes = _lib.query("abacus_rmsnorm_bwd_ws_bytes", rows, D)
+        ws = torch.empty(max(1, nbytes // 4), dtype=torch.float32, device=dy.device)
+        _lib.call("abacus_rmsnorm_bwd", _lib.ptr(dyc), _lib.ptr(xc), _lib.ptr(gamma.contiguous()), _lib.ptr(rstd),
+                  rows, D, _lib.dtype_code(xc.dtype), _lib.ptr(dx), _lib.ptr(dgamma), _lib.ptr(ws), nbytes,
+                  _lib.stream_of(dy.device))
+        return dx.view(dy.shape), dgamma, None
+
+
 class RMSNorm(torch.nn.Module):
-    """gamma * x / sqrt(mean(x^2) + 1e-5) over the last dimension (norm.py:11-31)."""
+    """gamma * x / sqrt(mean(x^2) + 1e-5) over the last dimension (norm.py:11-31).
+
+    On the GPU one fused HIP kernel each way (``abacus_rmsnorm_fwd`` / ``_bwd``);
+    on the CPU, or for inputs the kernel does not take, the reference's ops.
+    """
 
     def __init__(self, dim: int, sequence_parallel: bool = False, sync_grads: bool = False):
         super().__init__()
@@ -116,6 +168,8 @@ class RMSNorm(torch.nn.Module):
     def forward(self, x_BLD: torch.Tensor) -> torch.Tensor:
         if self.sync_grads and self.world_size > 1:
             _single_process("RMSNorm gradient synchronisation")
+        if _fused_norm_ok(x_BLD, self.w_gamma_D):
+            return _RMSNormFunction.apply(x_BLD, self.w_gamma_D, 1e-5)
         rms_BL = torch.sqrt(x_BLD.square().mean(dim=-1, keepdim=True) + 1e-5)  # (B, L, 1)
         return self.w_gamma_D * x_BLD / rms_BL
 
@@ -239,18 +293,21 @@ class MultiHeadAttention(torch.nn.Module):
         self.q_norm = RMSNorm(head_dim, sync_grads=sync_qk)
         self.k_norm = RMSNorm(head_dim, sync_grads=sync_qk)
 
-    def _split_heads(self, x_BLD: torch.Tensor, w_DHK: torch.Tensor) -> torch.Tensor:
+    def _split_heads(self, x_BLD: torch.Tensor, w_DHK: torch.Tensor, norm=None) -> torch.Tensor:
         B, L, _ = x_BLD.shape
         projected = x_BLD @ w_DHK.reshape(self.dim, self.local_heads * self.head_dim)  # (B, L, H*K)
-        return projected.view(B, L, self.local_heads, self.head_dim).permute(0, 2, 1, 3)  # (B, H, L, K)
+        heads = projected.view(B, L, self.local_heads, self.head_dim)
+        if norm is not None:  # per (b, l, h) row over K: the same before or after the permute
+            heads = norm(heads)
+        return heads.permute(0, 2, 1, 3)  # (B, H, L, K)
 
     def forward(self, x_BLD: torch.Tensor, rotary: Rotary | None = None) -> torch.Tensor:
         if self.context_parallel or self.world_size > 1:
             _single_process("attention parallelism")
         B, L, _ = x_BLD.shape
         H, K = self.local_heads, self.head_dim
-        q = self.q_norm(self._split_heads(x_BLD, self.w_q_DHK))
-        k = self.k_norm(self._split_heads(x_BLD, self.w_k_DHK))
+        q = self._split_heads(x_BLD, self.w_q_DHK, self.q_norm)
+        k = self._split_heads(x_BLD, self.w_k_DHK, self.k_norm)
         v = self._split_heads(x_BLD, self.w_v_DHK)
         if rotary is not None:
             cos, sin = rotary(q, seq_dim=2)

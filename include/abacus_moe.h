@@ -180,6 +180,25 @@ int abacus_moe_load_balancing_fwd(const void* probs_TE, const int64_t* slots_TK,
 int abacus_moe_load_balancing_bwd(const void* grad_loss, const float* f_E, int64_t T, int64_t E, float coeff_e,
                                   int dtype, void* grad_probs_TE, void* stream);
 
+/* ---- the decoder around the MoE layer ---------------------------------------- */
+
+/* RMSNorm.forward (norm.py:26-31): y = gamma * x / sqrt(mean(x^2) + eps) over
+ * the last dimension of `rows` contiguous rows of D elements (x, gamma and y
+ * in `dtype`), in fp32 with one rounding per output; rstd (rows fp32) gets
+ * 1 / sqrt(mean(x^2) + eps) for the backward.  D a multiple of 8 (bf16) or 4
+ * (fp32), at most 4096 (bf16) or 2048 (fp32). */
+int abacus_rmsnorm_fwd(const void* x, const void* gamma, int64_t rows, int64_t D, float eps, int dtype, void* y,
+                       float* rstd, void* stream);
+
+/* fp32 workspace bytes for abacus_rmsnorm_bwd. */
+int64_t abacus_rmsnorm_bwd_ws_bytes(int64_t rows, int64_t D);
+
+/* Autograd of RMSNorm.forward: dx = r * gamma * dy - x * r^3 * sum(gamma * dy * x) / D
+ * per row (r = rstd), dgamma = sum over rows of dy * x * r (added in a fixed
+ * order: deterministic). */
+int abacus_rmsnorm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, int64_t rows, int64_t D,
+                       int dtype, void* dx, void* dgamma, float* ws, int64_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

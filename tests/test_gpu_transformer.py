@@ -128,3 +128,39 @@ def test_attention_matches_materialised_fp64(dtype, shape):
         assert _rel(g, t) <= max(2 * _rel(r, t), rtol)
     if dtype == torch.bfloat16 and K == 64:
         assert tr._fused_ok.get((torch.bfloat16, 64)) is True, "fused attention did not run"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 5, 1024), (3, 7, 4, 64), (1, 3, 2048), (1, 2, 512), (0, 4, 1024), (2, 3, 72)],
+                         ids=["rows10_D1024", "rows84_D64", "D2048", "D512", "no_rows", "D72_fallback"])
+def test_rmsnorm_matches_fp64(dtype, shape):
+    """RMSNorm (norm.py:26-31) on the GPU -- the fused HIP kernel where it takes the
+    shape -- against fp64: output, dx and dgamma; and bitwise repeatable."""
+    from abacus_amd import transformer as tr
+    torch.manual_seed(7)
+    D = shape[-1]
+    norm = tr.RMSNorm(D)
+    with torch.no_grad():
+        norm.w_gamma_D.copy_(1 + 0.1 * torch.randn(D))
+    x = torch.randn(*shape)
+    g = torch.randn(*shape)
+
+    def run(mod, xx, gg):
+        xx = xx.clone().requires_grad_()
+        out = mod(xx)
+        out.backward(gg)
+        return [t.detach().double().cpu() for t in (out, xx.grad, mod.w_gamma_D.grad)]
+
+    gpu_mod = copy.deepcopy(norm).to(dtype).cuda()
+    got = run(gpu_mod, x.to(dtype).cuda(), g.to(dtype).cuda())
+    again = run(copy.deepcopy(norm).to(dtype).cuda(), x.to(dtype).cuda(), g.to(dtype).cuda())
+    ref = run(copy.deepcopy(norm).to(dtype), x.to(dtype), g.to(dtype))
+    tru = run(copy.deepcopy(norm).double(), x.double(), g.double())
+    rtol = RTOL[dtype]
+    for name, a, b, r, t in zip(("y", "dx", "dgamma"), got, again, ref, tru):
+        assert torch.equal(a, b), f"{name}: not bitwise repeatable"
+        if t.numel() == 0 or t.norm() == 0:
+            assert torch.count_nonzero(a) == 0
+            continue
+        assert _rel(a, t) <= max(2 * _rel(r, t), rtol), f"{name}: gpu {_rel(a, t):.3g} vs cpu {_rel(r, t):.3g}"
+    assert tr._fused_norm_ok(x.to(dtype).cuda(), gpu_mod.w_gamma_D) == (D != 72)
