@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_rmsnorm_fwd": (_I, [_P, _P, _I64, _I64, _F, _I, _P, _P, _P]),
     "abacus_rmsnorm_bwd_ws_bytes": (_I64, [_I64, _I64]),
     "abacus_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
+    "abacus_rmsnorm_rope_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P]),
+    "abacus_rmsnorm_rope_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
 }
 
 _lock = threading.Lock()

@@ -14,6 +14,14 @@
 // Layout: rows of D elements, contiguous.  A row is spread over LPR lanes of
 // a wave (LPR a power of two dividing the row's 16-byte vectors), each lane
 // holding VPL vectors; a wave covers 64 / LPR rows at a time.
+//
+// The attention's q and k norms can also apply the rotary embedding that
+// follows them (rope.py:36-46): for the (b, l, h) rows of a (B, L, H, K)
+// tensor, out = u * cos[l] + rotate_half(u) * sin[l] with u the normed row,
+// rotate_half(u) = (-u2, u1).  The backward first takes the transposed
+// rotation, du = g * cos + (g2 * sin2, -g1 * sin1) with g = dout, then the
+// norm's backward.  A row then sits on LPR lanes holding one vector each, so
+// element c's partner c +- K/2 is on lane li ^ (LPR / 2).
 #include <algorithm>
 
 #include "common.h"
@@ -52,11 +60,14 @@ __device__ inline float row_sum(float v, int lpr) {
   return v;
 }
 
-template <typename T, int VPL>
+template <typename T, int VPL, bool ROPE>
 __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_fwd_kernel(const T* __restrict__ x,
                                                                       const T* __restrict__ gamma, int64_t rows,
                                                                       int D, int lpr, float eps, T* __restrict__ y,
-                                                                      float* __restrict__ rstd) {
+                                                                      float* __restrict__ rstd,
+                                                                      const T* __restrict__ cosv,
+                                                                      const T* __restrict__ sinv, int L, int H) {
+  static_assert(!ROPE || VPL == 1, "the rotary pairs sit on partner lanes");
   constexpr int EPV = VecTraits<T>::kN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rpw = 64 / lpr, sub = lane / lpr, li = lane % lpr;
@@ -79,7 +90,25 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_fwd_kernel(const T* _
     }
     ss = row_sum(ss, lpr);
     const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-    if (act) {
+    if (ROPE) {
+      float f[EPV], gf[EPV], pf[EPV], cf[EPV], sf[EPV];
+      unpack<T>(xv[0], f);
+      unpack<T>(gv[0], gf);
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) f[i] = gf[i] * f[i] * inv;
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) pf[i] = __shfl_xor(f[i], lpr >> 1, 64);
+      if (act) {
+        const int64_t l = (r / H) % L;
+        unpack<T>(ld16(cosv + l * D + li * EPV), cf);
+        unpack<T>(ld16(sinv + l * D + li * EPV), sf);
+        const float sgn = li < (lpr >> 1) ? -1.0f : 1.0f;  // rotate_half: (-u2, u1)
+#pragma unroll
+        for (int i = 0; i < EPV; ++i) f[i] = f[i] * cf[i] + sgn * pf[i] * sf[i];
+        st16(y + r * D + li * EPV, pack<T>(f));
+        if (li == 0) rstd[r] = inv;
+      }
+    } else if (act) {
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         float f[EPV], gf[EPV];
@@ -94,13 +123,16 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_fwd_kernel(const T* _
   }
 }
 
-template <typename T, int VPL>
+template <typename T, int VPL, bool ROPE>
 __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* __restrict__ dy,
                                                                       const T* __restrict__ x,
                                                                       const T* __restrict__ gamma,
                                                                       const float* __restrict__ rstd, int64_t rows,
                                                                       int D, int lpr, T* __restrict__ dx,
-                                                                      float* __restrict__ partial) {
+                                                                      float* __restrict__ partial,
+                                                                      const T* __restrict__ cosv,
+                                                                      const T* __restrict__ sinv, int L, int H) {
+  static_assert(!ROPE || VPL == 1, "the rotary pairs sit on partner lanes");
   constexpr int EPV = VecTraits<T>::kN;
   constexpr int NE = VPL * EPV;  // elements per lane
   __shared__ float red_s[kNormWaves][64 * NE];
@@ -123,6 +155,20 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* _
       unpack<T>(act ? ld16(dy + o) : zero16(), df + v * EPV);
     }
     const float inv = act ? rstd[r] : 0.f;
+    if (ROPE) {
+      // gradient of the normed row through the rotation
+      float cf[EPV], sf[EPV], wv[EPV], pw[EPV];
+      const int64_t l = act ? (r / H) % L : 0;
+      unpack<T>(act ? ld16(cosv + l * D + li * EPV) : zero16(), cf);
+      unpack<T>(act ? ld16(sinv + l * D + li * EPV) : zero16(), sf);
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) wv[i] = df[i] * sf[i];
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) pw[i] = __shfl_xor(wv[i], lpr >> 1, 64);
+      const float sgn = li < (lpr >> 1) ? 1.0f : -1.0f;  // transposed rotate_half: (w2, -w1)
+#pragma unroll
+      for (int i = 0; i < EPV; ++i) df[i] = df[i] * cf[i] + sgn * pw[i];
+    }
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NE; ++i) s += gf[i] * df[i] * xf[i];
@@ -209,44 +255,51 @@ int64_t norm_groups(int64_t rows, int lpr) { return (rows + 64 / lpr - 1) / (64 
 
 using namespace abacus;
 
-extern "C" {
+namespace {
 
-int abacus_rmsnorm_fwd(const void* x, const void* gamma, int64_t rows, int64_t D, float eps, int dtype, void* y,
-                       float* rstd, void* stream) {
+int norm_fwd(const void* x, const void* gamma, int64_t rows, int64_t D, float eps, int dtype, void* y, float* rstd,
+             const void* cosv, const void* sinv, int64_t L, int64_t H, bool rope, void* stream) {
   int lpr, vpl;
   if (check_norm(rows, D, dtype, &lpr, &vpl)) return 1;
+  if (rope) {
+    ABACUS_CHECK_ARG(vpl == 1 && lpr >= 2 && L >= 1 && H >= 1,
+                     "rmsnorm_rope: head_dim %lld must be 2..64 16-byte vectors, a power of two", (long long)D);
+  }
   if (rows == 0) return 0;
   const int64_t groups = norm_groups(rows, lpr);
   const unsigned grid = (unsigned)std::min<int64_t>(kNormMaxBlocks, (groups + kNormWaves - 1) / kNormWaves);
   hipStream_t s = (hipStream_t)stream;
-#define ABACUS_NORM_FWD(TT, V)                                                                                    \
-  hipLaunchKernelGGL((rmsnorm_fwd_kernel<TT, V>), dim3(grid), dim3(kNormWaves * 64), 0, s, (const TT*)x,          \
-                     (const TT*)gamma, rows, (int)D, lpr, eps, (TT*)y, rstd)
+#define ABACUS_NORM_FWD(TT, V, R)                                                                                 \
+  hipLaunchKernelGGL((rmsnorm_fwd_kernel<TT, V, R>), dim3(grid), dim3(kNormWaves * 64), 0, s, (const TT*)x,       \
+                     (const TT*)gamma, rows, (int)D, lpr, eps, (TT*)y, rstd, (const TT*)cosv, (const TT*)sinv,   \
+                     (int)L, (int)H)
   if (dtype == kBF16) {
-    if (vpl == 1) ABACUS_NORM_FWD(uint16_t, 1);
-    else if (vpl == 2) ABACUS_NORM_FWD(uint16_t, 2);
-    else if (vpl == 4) ABACUS_NORM_FWD(uint16_t, 4);
-    else ABACUS_NORM_FWD(uint16_t, 8);
+    if (rope) ABACUS_NORM_FWD(uint16_t, 1, true);
+    else if (vpl == 1) ABACUS_NORM_FWD(uint16_t, 1, false);
+    else if (vpl == 2) ABACUS_NORM_FWD(uint16_t, 2, false);
+    else if (vpl == 4) ABACUS_NORM_FWD(uint16_t, 4, false);
+    else ABACUS_NORM_FWD(uint16_t, 8, false);
   } else {
-    if (vpl == 1) ABACUS_NORM_FWD(float, 1);
-    else if (vpl == 2) ABACUS_NORM_FWD(float, 2);
-    else if (vpl == 4) ABACUS_NORM_FWD(float, 4);
-    else ABACUS_NORM_FWD(float, 8);
+    if (rope) ABACUS_NORM_FWD(float, 1, true);
+    else if (vpl == 1) ABACUS_NORM_FWD(float, 1, false);
+    else if (vpl == 2) ABACUS_NORM_FWD(float, 2, false);
+    else if (vpl == 4) ABACUS_NORM_FWD(float, 4, false);
+    else ABACUS_NORM_FWD(float, 8, false);
   }
 #undef ABACUS_NORM_FWD
   ABACUS_CHECK_LAUNCH("rmsnorm_fwd");
   return 0;
 }
 
-int64_t abacus_rmsnorm_bwd_ws_bytes(int64_t rows, int64_t D) {
-  if (rows <= 0 || D <= 0) return 0;
-  return (int64_t)kNormBwdBlocks * D * 4;
-}
-
-int abacus_rmsnorm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, int64_t rows, int64_t D,
-                       int dtype, void* dx, void* dgamma, float* ws, int64_t ws_bytes, void* stream) {
+int norm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, int64_t rows, int64_t D, int dtype,
+             void* dx, void* dgamma, float* ws, int64_t ws_bytes, const void* cosv, const void* sinv, int64_t L,
+             int64_t H, bool rope, void* stream) {
   int lpr, vpl;
   if (check_norm(rows, D, dtype, &lpr, &vpl)) return 1;
+  if (rope) {
+    ABACUS_CHECK_ARG(vpl == 1 && lpr >= 2 && L >= 1 && H >= 1,
+                     "rmsnorm_rope: head_dim %lld must be 2..64 16-byte vectors, a power of two", (long long)D);
+  }
   hipStream_t s = (hipStream_t)stream;
   const int64_t groups = norm_groups(rows, lpr);
   const int nb = (int)std::max<int64_t>(1, std::min<int64_t>(kNormBwdBlocks, (groups + kNormWaves - 1) / kNormWaves));
@@ -263,19 +316,22 @@ int abacus_rmsnorm_bwd(const void* dy, const void* x, const void* gamma, const f
     ABACUS_CHECK_LAUNCH("rmsnorm_dgamma");
     return 0;
   }
-#define ABACUS_NORM_BWD(TT, V)                                                                                     \
-  hipLaunchKernelGGL((rmsnorm_bwd_kernel<TT, V>), dim3(nb), dim3(kNormWaves * 64), 0, s, (const TT*)dy,            \
-                     (const TT*)x, (const TT*)gamma, rstd, rows, (int)D, lpr, (TT*)dx, ws)
+#define ABACUS_NORM_BWD(TT, V, R)                                                                                  \
+  hipLaunchKernelGGL((rmsnorm_bwd_kernel<TT, V, R>), dim3(nb), dim3(kNormWaves * 64), 0, s, (const TT*)dy,         \
+                     (const TT*)x, (const TT*)gamma, rstd, rows, (int)D, lpr, (TT*)dx, ws, (const TT*)cosv,        \
+                     (const TT*)sinv, (int)L, (int)H)
   if (dtype == kBF16) {
-    if (vpl == 1) ABACUS_NORM_BWD(uint16_t, 1);
-    else if (vpl == 2) ABACUS_NORM_BWD(uint16_t, 2);
-    else if (vpl == 4) ABACUS_NORM_BWD(uint16_t, 4);
-    else ABACUS_NORM_BWD(uint16_t, 8);
+    if (rope) ABACUS_NORM_BWD(uint16_t, 1, true);
+    else if (vpl == 1) ABACUS_NORM_BWD(uint16_t, 1, false);
+    else if (vpl == 2) ABACUS_NORM_BWD(uint16_t, 2, false);
+    else if (vpl == 4) ABACUS_NORM_BWD(uint16_t, 4, false);
+    else ABACUS_NORM_BWD(uint16_t, 8, false);
   } else {
-    if (vpl == 1) ABACUS_NORM_BWD(float, 1);
-    else if (vpl == 2) ABACUS_NORM_BWD(float, 2);
-    else if (vpl == 4) ABACUS_NORM_BWD(float, 4);
-    else ABACUS_NORM_BWD(float, 8);
+    if (rope) ABACUS_NORM_BWD(float, 1, true);
+    else if (vpl == 1) ABACUS_NORM_BWD(float, 1, false);
+    else if (vpl == 2) ABACUS_NORM_BWD(float, 2, false);
+    else if (vpl == 4) ABACUS_NORM_BWD(float, 4, false);
+    else ABACUS_NORM_BWD(float, 8, false);
   }
 #undef ABACUS_NORM_BWD
   ABACUS_CHECK_LAUNCH("rmsnorm_bwd");
@@ -287,6 +343,37 @@ int abacus_rmsnorm_bwd(const void* dy, const void* x, const void* gamma, const f
                        (int)D, (float*)dgamma);
   ABACUS_CHECK_LAUNCH("rmsnorm_dgamma");
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t abacus_rmsnorm_bwd_ws_bytes(int64_t rows, int64_t D) {
+  if (rows <= 0 || D <= 0) return 0;
+  return (int64_t)kNormBwdBlocks * D * 4;
+}
+
+int abacus_rmsnorm_fwd(const void* x, const void* gamma, int64_t rows, int64_t D, float eps, int dtype, void* y,
+                       float* rstd, void* stream) {
+  return norm_fwd(x, gamma, rows, D, eps, dtype, y, rstd, nullptr, nullptr, 1, 1, false, stream);
+}
+
+int abacus_rmsnorm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, int64_t rows, int64_t D,
+                       int dtype, void* dx, void* dgamma, float* ws, int64_t ws_bytes, void* stream) {
+  return norm_bwd(dy, x, gamma, rstd, rows, D, dtype, dx, dgamma, ws, ws_bytes, nullptr, nullptr, 1, 1, false, stream);
+}
+
+int abacus_rmsnorm_rope_fwd(const void* x, const void* gamma, const void* cos_LK, const void* sin_LK, int64_t rows,
+                            int64_t L, int64_t H, int64_t K, float eps, int dtype, void* y, float* rstd,
+                            void* stream) {
+  return norm_fwd(x, gamma, rows, K, eps, dtype, y, rstd, cos_LK, sin_LK, L, H, true, stream);
+}
+
+int abacus_rmsnorm_rope_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, const void* cos_LK,
+                            const void* sin_LK, int64_t rows, int64_t L, int64_t H, int64_t K, int dtype, void* dx,
+                            void* dgamma, float* ws, int64_t ws_bytes, void* stream) {
+  return norm_bwd(dy, x, gamma, rstd, rows, K, dtype, dx, dgamma, ws, ws_bytes, cos_LK, sin_LK, L, H, true, stream);
 }
 
 }  // extern "C"

@@ -150,6 +150,49 @@ class _RMSNormFunction(torch.autograd.Function):
         return dx.view(dy.shape), dgamma, None
 
 
+def _fused_rope_ok(x: torch.Tensor, gamma: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> bool:
+    """The HIP norm + rotary kernel takes what the fused norm takes, with cos/sin of
+    x's dtype and a row of 2..64 16-byte vectors, a power of two (one per lane)."""
+    if not (_fused_norm_ok(x, gamma) and cos.dtype == x.dtype and sin.dtype == x.dtype):
+        return False
+    nvec = x.shape[-1] // (8 if x.dtype == torch.bfloat16 else 4)
+    return 2 <= nvec <= 64 and nvec & (nvec - 1) == 0
+
+
+class _RMSNormRopeFunction(torch.autograd.Function):
+    """RMSNorm over K of a (B, L, H, K) tensor, then the rotary embedding at each
+    row's position l: one HIP kernel each way."""
+
+    @staticmethod
+    def forward(ctx, x_BLHK, gamma, cos_LK, sin_LK, eps: float):
+        B, L, H, K = x_BLHK.shape
+        xc = x_BLHK.contiguous()
+        rows = B * L * H
+        y = torch.empty_like(xc)
+        rstd = torch.empty(rows, dtype=torch.float32, device=xc.device)
+        cos_c, sin_c = cos_LK.contiguous(), sin_LK.contiguous()
+        _lib.call("abacus_rmsnorm_rope_fwd", _lib.ptr(xc), _lib.ptr(gamma.contiguous()), _lib.ptr(cos_c),
+                  _lib.ptr(sin_c), rows, L, H, K, eps, _lib.dtype_code(xc.dtype), _lib.ptr(y), _lib.ptr(rstd),
+                  _lib.stream_of(xc.device))
+        ctx.save_for_backward(xc, gamma, rstd, cos_c, sin_c)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        xc, gamma, rstd, cos_c, sin_c = ctx.saved_tensors
+        B, L, H, K = xc.shape
+        rows = B * L * H
+        dyc = dy.contiguous()
+        dx = torch.empty_like(xc)
+        dgamma = torch.empty_like(gamma)
+        nbytes = _lib.query("abacus_rmsnorm_bwd_ws_bytes", rows, K)
+        ws = torch.empty(max(1, nbytes // 4), dtype=torch.float32, device=dy.device)
+        _lib.call("abacus_rmsnorm_rope_bwd", _lib.ptr(dyc), _lib.ptr(xc), _lib.ptr(gamma.contiguous()),
+                  _lib.ptr(rstd), _lib.ptr(cos_c), _lib.ptr(sin_c), rows, L, H, K, _lib.dtype_code(xc.dtype),
+                  _lib.ptr(dx), _lib.ptr(dgamma), _lib.ptr(ws), nbytes, _lib.stream_of(dy.device))
+        return dx, dgamma, None, None, None
+
+
 class RMSNorm(torch.nn.Module):
     """gamma * x / sqrt(mean(x^2) + 1e-5) over the last dimension (norm.py:11-31).
 
@@ -306,12 +349,23 @@ class MultiHeadAttention(torch.nn.Module):
             _single_process("attention parallelism")
         B, L, _ = x_BLD.shape
         H, K = self.local_heads, self.head_dim
-        q = self._split_heads(x_BLD, self.w_q_DHK, self.q_norm)
-        k = self._split_heads(x_BLD, self.w_k_DHK, self.k_norm)
         v = self._split_heads(x_BLD, self.w_v_DHK)
+        q_heads = (x_BLD @ self.w_q_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
+        k_heads = (x_BLD @ self.w_k_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
+        cos = sin = None
         if rotary is not None:
-            cos, sin = rotary(q, seq_dim=2)
-            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            cos, sin = rotary(q_heads, seq_dim=1)  # (1, 1, L, K)
+        if (cos is not None and _fused_rope_ok(q_heads, self.q_norm.w_gamma_D, cos, sin)
+                and _fused_rope_ok(k_heads, self.k_norm.w_gamma_D, cos, sin)):
+            # q/k norm and the rotary embedding in one HIP kernel each
+            cos_LK, sin_LK = cos.reshape(L, K), sin.reshape(L, K)
+            q = _RMSNormRopeFunction.apply(q_heads, self.q_norm.w_gamma_D, cos_LK, sin_LK, 1e-5).permute(0, 2, 1, 3)
+            k = _RMSNormRopeFunction.apply(k_heads, self.k_norm.w_gamma_D, cos_LK, sin_LK, 1e-5).permute(0, 2, 1, 3)
+        else:
+            q = self.q_norm(q_heads).permute(0, 2, 1, 3)  # (B, H, L, K)
+            k = self.k_norm(k_heads).permute(0, 2, 1, 3)
+            if rotary is not None:
+                q, k = apply_rotary_pos_emb(q, k, cos, sin)
         out = _fused_causal_attention(q, k, v) if q.is_cuda else None  # (B, H, L, K)
         if out is None:
             out = _CausalAttention.apply(

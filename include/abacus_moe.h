@@ -199,6 +199,21 @@ int64_t abacus_rmsnorm_bwd_ws_bytes(int64_t rows, int64_t D);
 int abacus_rmsnorm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, int64_t rows, int64_t D,
                        int dtype, void* dx, void* dgamma, float* ws, int64_t ws_bytes, void* stream);
 
+/* The attention's q/k norm followed by the rotary embedding
+ * (attention.py:126-131, rope.py:36-46): for the rows = B*L*H rows (b, l, h)
+ * of a contiguous (B, L, H, K) tensor, out = u * cos[l] + rotate_half(u) * sin[l]
+ * with u = RMSNorm(row) as above and cos_LK, sin_LK (L, K) in `dtype`.  K/8 (bf16)
+ * or K/4 (fp32) a power of two from 2 to 64. */
+int abacus_rmsnorm_rope_fwd(const void* x, const void* gamma, const void* cos_LK, const void* sin_LK, int64_t rows,
+                            int64_t L, int64_t H, int64_t K, float eps, int dtype, void* y, float* rstd,
+                            void* stream);
+
+/* Autograd of abacus_rmsnorm_rope_fwd: the transposed rotation of dy, then the
+ * norm's backward (workspace: abacus_rmsnorm_bwd_ws_bytes(rows, K)). */
+int abacus_rmsnorm_rope_bwd(const void* dy, const void* x, const void* gamma, const float* rstd, const void* cos_LK,
+                            const void* sin_LK, int64_t rows, int64_t L, int64_t H, int64_t K, int dtype, void* dx,
+                            void* dgamma, float* ws, int64_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

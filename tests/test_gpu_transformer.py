@@ -164,3 +164,41 @@ def test_rmsnorm_matches_fp64(dtype, shape):
             continue
         assert _rel(a, t) <= max(2 * _rel(r, t), rtol), f"{name}: gpu {_rel(a, t):.3g} vs cpu {_rel(r, t):.3g}"
     assert tr._fused_norm_ok(x.to(dtype).cuda(), gpu_mod.w_gamma_D) == (D != 72)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 9, 3, 64), (1, 33, 2, 16), (2, 5, 4, 128)], ids=["K64", "K16", "K128"])
+def test_rmsnorm_rope_matches_fp64(dtype, shape):
+    """The fused q/k norm + rotary kernel against RMSNorm then apply_rotary_pos_emb
+    (norm.py:26-31, rope.py:36-46) in fp64: output, dx and dgamma."""
+    from abacus_amd import transformer as tr
+    B, L, H, K = shape
+    torch.manual_seed(8)
+    gamma = 1 + 0.1 * torch.randn(K)
+    x = torch.randn(B, L, H, K)
+    g = torch.randn(B, L, H, K)
+    rot = tr.Rotary(K)
+    cos, sin = rot(x, seq_dim=1)  # (1, 1, L, K) fp32
+
+    def composite(xx, gm, c, s_):
+        rms = torch.sqrt(xx.square().mean(-1, keepdim=True) + 1e-5)
+        u = (gm * xx / rms).permute(0, 2, 1, 3)  # (B, H, L, K)
+        out, _ = tr.apply_rotary_pos_emb(u, u, c, s_)
+        return out.permute(0, 2, 1, 3)
+
+    def run(fn, dev, dt):
+        xx = x.detach().to(dev, dt).clone().requires_grad_()
+        gm = gamma.detach().to(dev, dt).clone().requires_grad_()
+        out = fn(xx, gm, cos.to(dev, dt), sin.to(dev, dt))
+        out.backward(g.to(dev, dt))
+        return [t.detach().double().cpu() for t in (out, xx.grad, gm.grad)]
+
+    c_dev, s_dev = cos.to("cuda", dtype), sin.to("cuda", dtype)
+    assert tr._fused_rope_ok(x.to("cuda", dtype), gamma.to("cuda", dtype), c_dev, s_dev)
+    got = run(lambda xx, gm, c, s_: tr._RMSNormRopeFunction.apply(xx, gm, c.reshape(L, K), s_.reshape(L, K), 1e-5),
+              "cuda", dtype)
+    ref = run(composite, "cpu", dtype)
+    tru = run(composite, "cpu", torch.float64)
+    rtol = RTOL[dtype]
+    for name, a, r, t in zip(("y", "dx", "dgamma"), got, ref, tru):
+        assert _rel(a, t) <= max(2 * _rel(r, t), rtol), f"{name}: gpu {_rel(a, t):.3g} vs cpu {_rel(r, t):.3g}"
