@@ -21,6 +21,7 @@
 // a single ds_read_b128.  bf16 uses v_mfma_f32_16x16x32_bf16, fp32 uses
 // v_mfma_f32_16x16x4_f32; accumulation is always fp32.
 #include <algorithm>
+#include <atomic>
 
 #include "common.h"
 
@@ -82,6 +83,9 @@ struct GemmArgs {
   // Pipelined kernel, row-grouped kinds: nonzero when expert remainders of at
   // most THIN rows go to thin tiles (else every row tile is a full one).
   int thin;
+  // Pipelined kernel, weight gradients: this launch's set of tile counters
+  // (pipe::g_tile_ctr).
+  int ctr_slot;
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -1104,17 +1108,282 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   }
 }
 
+
+// ---------------- weight gradients: a persistent tile loop ----------------
+// A weight gradient's tile reduces over one expert's rows only (about 1000 at
+// the Mixtral shape: 16 k-tiles, ~30 us of MFMA work), so a block per tile
+// would pay a block launch, its first DMA's latency and its epilogue every
+// ~30 us.  Instead P blocks (one per CU) loop over tiles they claim from
+// per-XCD counters: each XCD's blocks walk that XCD's contiguous share of the
+// logical tiles (the L2 grouping of xcd_logical), and a block whose share is
+// used up takes tiles from the other XCDs' shares, so blocks that start late
+// (behind the long tiles of a pair launch) still end together.  A block
+// claims its next tile while it stages the finished one through LDS and
+// issues the next tile's first DMA before the finished tile's stores, so the
+// DMA latency and the stores overlap.
+//
+// Counters: one set per launch slot.  The host gives consecutive launches
+// consecutive slots, so launches in flight on different streams use different
+// counters; the last of a launch's P blocks to finish sets its slot back to
+// zero for the next launch that uses it.
+constexpr int kCtrSlots = 64;
+constexpr int kMaxExperts = 4096;  // the expert offsets a block keeps in LDS (check_gemm_shape's bound)
+__device__ int g_tile_ctr[kCtrSlots][16] = {};  // [0..7] next tile of each XCD's share, [8] blocks done
+
+__device__ inline int xcc_id() { return __builtin_amdgcn_s_getreg((31 << 11) | 20) & 7; }  // HW_REG_XCC_ID
+
+// Thread 0: claims the next tile for a block on XCD `xcc` (-1: every share is
+// used up).  `from` is the block's scan position over the shares, own first.
+__device__ inline int claim_tile(int* ctr, int xcc, int& from, int per, int total) {
+  for (; from < 8; ++from) {
+    const int c = (xcc + from) & 7;
+    const int n = min(per, total - c * per);
+    if (n > 0) {
+      const int t = atomicAdd(&ctr[c], 1);
+      if (t < n) return c * per + t;
+    }
+  }
+  return -1;
+}
+
+// The weight-gradient tiles of g (KindTraits WGRAD) on P blocks of this
+// launch.  Every one of the P blocks must call it.  LDS beyond lds: next_s,
+// one int; offs_s, kMaxExperts + 1 ints (the expert offsets, so that starting
+// a tile waits on no global load).
 template <int KIND>
-__global__ __launch_bounds__(NT, 1) void gemm_bf16_kernel(GemmArgs g) {
+__device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const GemmArgs& g, int P, char* lds,
+                                                                       int* next_s, int* offs_s) {
+  using KT = KindTraits<KIND>;
+  using Op = MfmaOp<uint16_t, 32>;
+  using GE = Geo<BM>;
+  static_assert(KT::WGRAD && KT::A_MC && KT::B_NC && !KT::DUAL_K, "weight-gradient kinds");
+  constexpr int STAGE_BYTES = GE::STAGE, A_BYTES = GE::A_BYTES, LOADS_PER_TILE = GE::LOADS, DMA_A = GE::DMA_A;
+  constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;
+
+  int tid = threadIdx.x;
+  int lane = tid & 63;
+  int wave = tid >> 6;
+  int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // Re-derives the lane-dependent indices from an opaque copy of the thread
+  // index at the top of each tile, so the per-lane addresses they feed are
+  // computed again per tile instead of being hoisted out of the tile loop and
+  // held in registers across it (which spills).
+  auto refresh = [&]() __attribute__((always_inline)) {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    tid = t;
+    lane = t & 63;
+    wave = t >> 6;
+    wm = wave / WAVES_N;
+    wn = wave % WAVES_N;
+    wave_u = __builtin_amdgcn_readfirstlane(wave);
+  };
+
+  int* ctr = g_tile_ctr[g.ctr_slot];
+  const int total = g.E * g.tiles_m * g.tiles_n;  // logical tiles, padding included
+  const int per = (total + 7) / 8;
+  const int xcc = xcc_id();
+  int from = 0;
+
+  // logical tile -> (expert, output rows, output columns); false: padding
+  auto decode = [&](int L, int& e_, int& row0_, int& n0_) __attribute__((always_inline)) -> bool {
+    const TileId tl = tile_of_logical(L, g.tiles_m, g.tiles_n);
+    e_ = tl.e;
+    row0_ = tl.mt * BM;
+    n0_ = tl.nt * BNH;
+    return e_ < g.E && row0_ < g.Mdim && n0_ < g.Ndim;
+  };
+  auto claim = [&]() __attribute__((always_inline)) -> int {  // thread 0
+    for (;;) {
+      const int L = claim_tile(ctr, xcc, from, per, total);
+      int a, b, c;
+      if (L < 0 || decode(L, a, b, c)) return L;
+    }
+  };
+
+  int e = 0, row0 = 0, n0 = 0, k_len = 0, ktiles = 0;
+  DmaStream<true, DMA_A> sa;
+  DmaStream<true> sb;
+  char* dma_stage = lds;
+  int dma_k0 = 0;
+  auto prep = [&](int kt) __attribute__((always_inline)) {
+    dma_stage = lds + (kt % STAGES) * STAGE_BYTES;
+    dma_k0 = kt * BK;
+  };
+  auto dma = [&](int n) __attribute__((always_inline)) {
+    if (n < DMA_A) sa.template issue_one<true>(n, dma_stage, wave_u, dma_k0, k_len);
+    else sb.template issue_one<true>(n - DMA_A, dma_stage + A_BYTES, wave_u, dma_k0, k_len);
+  };
+  // Tile L: its expert's row segment, DMA sources, and the DMA of its first
+  // STAGES k-tiles.
+  auto begin = [&](int L) __attribute__((always_inline)) {
+    decode(L, e, row0, n0);
+    const int seg0 = offs_s[e];
+    k_len = offs_s[e + 1] - seg0;
+    ktiles = (k_len + BK - 1) / BK;
+    const uint16_t* A0 = (const uint16_t*)g.a0 + (int64_t)seg0 * g.lda;
+    const uint16_t* B0 = (const uint16_t*)g.b0 + (int64_t)seg0 * g.ldb;
+    const uint16_t* B1 = KT::DUAL_B ? (const uint16_t*)g.b1 + (int64_t)seg0 * g.ldb : nullptr;
+    sa.setup(A0, nullptr, g.lda, row0, g.Mdim, wave, lane);
+    sb.setup(B0, B1, g.ldb, n0, g.Ndim, wave, lane);
+#pragma unroll
+    for (int p = 0; p < STAGES; ++p)
+      if (p < ktiles) {
+        prep(p);
+#pragma unroll
+        for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
+      }
+  };
+
+  Op::Acc acc[FM][FN];
+  auto b_col = [&](int j) __attribute__((always_inline)) -> int {
+    if (KT::DUAL_B) {
+      constexpr int HF = FN / 2;
+      return (j / HF) * (BN / 2) + wn * HF * 32 + (j % HF) * 32;
+    }
+    return wn * WTN + j * 32;
+  };
+  Vec16 af[2][FM], bfr[2][FN];
+  constexpr int NFRAG = FM + FN;
+  auto read_frag = [&](const char* st, int t, int slot, int f) __attribute__((always_inline)) {
+    if (f == 0 || f > FN) {
+      const int i = f == 0 ? 0 : f - FN;
+      af[slot][i] = frag_mc(st, wm * WTM + i * 32, t, lane);
+    } else {
+      const int j = f - 1;
+      bfr[slot][j] = frag_mc(st + A_BYTES, b_col(j), t, lane);
+    }
+  };
+  // the k-step and k-tile schedule of gemm_tile
+  auto kstep = [&](int slot, bool with_read, const char* rd_st, int rd_t, int rd_slot, bool with_dma) __attribute__((always_inline)) {
+    constexpr int MF = FM * FN;
+#pragma unroll
+    for (int m = 0; m < MF; ++m) {
+      Op::run(acc[m / FN][m % FN], bfr[slot][m % FN], af[slot][m / FN]);
+      if (with_read && m < NFRAG) read_frag(rd_st, rd_t, rd_slot, m);
+      if (with_dma) {
+#pragma unroll
+        for (int n = m * LOADS_PER_TILE / MF; n < (m + 1) * LOADS_PER_TILE / MF; ++n) dma(n);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto ktile = [&](int kt, bool next, bool dma_next) __attribute__((always_inline)) {
+    const char* st = lds + (kt % STAGES) * STAGE_BYTES;
+    const char* st_next = lds + ((kt + 1) % STAGES) * STAGE_BYTES;
+#pragma unroll
+    for (int t = 0; t < NSTEP - 1; ++t) kstep(t & 1, true, st, t + 1, (t + 1) & 1, false);
+    wait_vmcnt<0>();  // (two stages: tile kt+1 is the newest in flight)
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __syncthreads();
+    if (dma_next) prep(kt + STAGES);
+    __builtin_amdgcn_sched_barrier(0);
+    kstep((NSTEP - 1) & 1, next, st_next, 0, 0, dma_next);
+  };
+  static_assert(STAGES == 2, "the persistent loop waits for every DMA in flight");
+
+  constexpr int CVR = BN / 8;          // 16-byte vectors per C-tile row
+  constexpr int NVA = BM * CVR / NT;   // per thread
+  static_assert(NT % CVR == 0, "a thread's vectors share one C-tile column");
+  uint16_t* ctile = reinterpret_cast<uint16_t*>(lds);
+
+  for (int i = tid; i <= g.E; i += NT) offs_s[i] = g.offsets[i];
+  if (tid == 0) *next_s = claim();
+  __syncthreads();
+  int L = __builtin_amdgcn_readfirstlane(*next_s);
+  if (L >= 0) begin(L);
+  while (L >= 0) {
+    refresh();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < Op::kAcc; ++q) acc[i][j][q] = 0.f;
+    if (ktiles > 0) {
+      wait_vmcnt<0>();  // this tile's first k-tiles (and the previous tile's stores)
+      __syncthreads();
+#pragma unroll
+      for (int f = 0; f < NFRAG; ++f) read_frag(lds, 0, 0, f);
+      int kt = 0;
+      for (; kt + STAGES < ktiles; ++kt) ktile(kt, true, true);
+      for (; kt + 1 < ktiles; ++kt) ktile(kt, true, false);
+      ktile(kt, false, false);
+    }
+    __syncthreads();  // every fragment read done: the C tile may overwrite the stages
+
+    // claim the next tile (thread 0; the atomic is in flight while the C
+    // tile is written), stage the C tile, and read it back into registers
+    int Ln = -1;
+    if (tid == 0) Ln = claim();
+    {
+      const int rl = lane & 31, ch = 4 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            uint2 w;
+            w.x = pack_bf16x2(acc[i][j][4 * gq], acc[i][j][4 * gq + 1]);
+            w.y = pack_bf16x2(acc[i][j][4 * gq + 2], acc[i][j][4 * gq + 3]);
+            *reinterpret_cast<uint2*>(ctile + (wm * WTM + i * 32 + rl) * LDC + b_col(j) + 8 * gq + ch) = w;
+          }
+    }
+    if (tid == 0) *next_s = Ln;
+    __syncthreads();
+    // (word by word: a whole-struct copy from LDS keeps cv in scratch)
+    Vec16 cv[NVA];
+#pragma unroll
+    for (int u = 0; u < NVA; ++u) {
+      const int v = tid + u * NT;
+      const uint4 x = *reinterpret_cast<const uint4*>(ctile + (v / CVR) * LDC + (v % CVR) * 8);
+      cv[u].w[0] = x.x;
+      cv[u].w[1] = x.y;
+      cv[u].w[2] = x.z;
+      cv[u].w[3] = x.w;
+    }
+    Ln = __builtin_amdgcn_readfirstlane(*next_s);
+    __syncthreads();  // every C-tile read done: the next tile's DMA may refill the stages
+
+    const int e_c = e, row0_c = row0, n0_c = n0;
+    if (Ln >= 0) begin(Ln);
+    // column v % CVR of the C tile: for dual-B kinds the first BNH columns
+    // are the gate output's, the rest the up output's
+    const int cc = (tid % CVR) * 8;
+    const bool up_half = KT::DUAL_B && cc >= BNH;
+    uint16_t* out = (uint16_t*)(up_half ? g.c1 : g.c0) + (int64_t)e_c * g.c_estride;
+    const int col = n0_c + (up_half ? cc - BNH : cc);
+#pragma unroll
+    for (int u = 0; u < NVA; ++u) {
+      const int row = row0_c + (tid + u * NT) / CVR;
+      if (row < g.Mdim && col < g.Ndim) st16(out + (int64_t)row * g.ldc + col, cv[u]);
+    }
+    L = Ln;
+  }
+
+  // the last block out sets the counters back to zero
+  if (tid == 0 && atomicAdd(&ctr[8], 1) == P - 1) {
+#pragma unroll
+    for (int c = 0; c < 9; ++c) atomicExch(&ctr[c], 0);
+  }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(NT, 1) void gemm_bf16_wgrad_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
-  gemm_tile<KIND>(g, blockIdx.x, gridDim.x, lds);
+  __shared__ int next_s;
+  __shared__ int offs_s[kMaxExperts + 1];
+  gemm_wgrad_tiles<KIND>(g, (int)gridDim.x, lds, &next_s, offs_s);
 }
 
 // A row-grouped kind's full tiles, then its thin tiles, then (KW >= 0) a
 // weight gradient's tiles, in one launch: blocks [0, n1), [n1, n1 + n2), and
-// the rest (n1 and n2 multiples of 8).  Blocks are dispatched in index order,
-// so the long tiles go first and the shorter ones fill the CUs that the long
-// tiles' last partial round would leave idle.
+// the rest (n1 and n2 multiples of 8), the last as a persistent loop
+// (gemm_wgrad_tiles).  Blocks are dispatched in index order, so the long
+// tiles go first and the weight gradient's blocks start on the CUs that the
+// long tiles' last partial round leaves idle.
 template <int KR, int KW>
 __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, GemmArgs g2, GemmArgs g3, int n1,
                                                                int n2) {
@@ -1125,7 +1394,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, Gemm
   } else if (b < n1 + n2) {
     gemm_tile<KR, THIN>(g2, b - n1, n2, lds);
   } else {
-    if constexpr (KW >= 0) gemm_tile<KW, BM>(g3, b - n1 - n2, (int)gridDim.x - n1 - n2, lds);
+    if constexpr (KW >= 0) {
+      __shared__ int next_s;
+      __shared__ int offs_s[kMaxExperts + 1];
+      gemm_wgrad_tiles<KW>(g3, (int)gridDim.x - n1 - n2, lds, &next_s, offs_s);
+    }
   }
 }
 
@@ -1217,6 +1490,26 @@ int64_t pipe_grid(GemmArgs& g, int R) {
   return (int64_t)(KT::WGRAD ? g.E : 1) * g.tiles_m * g.tiles_n;
 }
 
+// Counter slot of a persistent weight-gradient launch: consecutive launches
+// take consecutive slots.
+inline int next_ctr_slot() {
+  static std::atomic<unsigned> seq{0};
+  return (int)(seq.fetch_add(1, std::memory_order_relaxed) % pipe::kCtrSlots);
+}
+
+inline int cu_count();
+
+// Blocks of a persistent weight-gradient launch (one per CU, at most one per
+// tile); sizes its tile space and takes its counter slot.  0: no tiles.
+template <int KIND>
+int64_t wgrad_blocks(GemmArgs& g, int R) {
+  static_assert(KindTraits<KIND>::WGRAD, "weight-gradient kinds");
+  const int64_t total = pipe_grid<KIND>(g, R);
+  if (total == 0) return 0;
+  g.ctr_slot = next_ctr_slot();
+  return std::min<int64_t>(cu_count(), total);
+}
+
 // The thin row tiles of a row-grouped kind: at most one per expert, in the
 // same column tiles.  Returns the number of blocks, a multiple of 8.
 template <int KIND>
@@ -1239,7 +1532,11 @@ int launch_rows(const GemmArgs& g1, int R, const GemmArgs* gw, int64_t n1, bool 
   const int64_t full = pipe_grid<KR>(ga, R);
   if (n1 < 0) n1 = full;  // no split: one block per full tile of the upper bound
   const int64_t n2 = thin ? pipe_grid_thin<KR>(gt, R) : 0;
-  const int64_t n3 = KW >= 0 ? pipe_grid<(KW >= 0 ? KW : KR)>(gc, R) : 0;
+  int64_t n3 = 0;
+  if constexpr (KW >= 0) {
+    n3 = wgrad_blocks<KW>(gc, R);
+    ABACUS_CHECK_ARG((int64_t)gc.E * gc.tiles_m * gc.tiles_n < (1ll << 31), "%s: tile grid too large", name);
+  }
   ABACUS_CHECK_ARG(n1 + n2 + n3 < (1ll << 31), "%s: tile grid too large", name);
   if (n1 + n2 + n3 == 0) return 0;
   hipLaunchKernelGGL((pipe::gemm_bf16_rows_kernel<KR, KW>), dim3((unsigned)(n1 + n2 + n3)), dim3(pipe::NT), 0, s, ga,
@@ -1256,10 +1553,10 @@ int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
     return launch_rows<KIND, -1>(g, R, nullptr, -1, KIND != kDownFwd, s, name);
   } else {
     GemmArgs ga = g;
-    const int64_t total = pipe_grid<KIND>(ga, R);
-    if (total == 0) return 0;
-    ABACUS_CHECK_ARG(total < (1ll << 31), "%s: tile grid too large", name);
-    hipLaunchKernelGGL(pipe::gemm_bf16_kernel<KIND>, dim3((unsigned)total), dim3(pipe::NT), 0, s, ga);
+    const int64_t blocks = wgrad_blocks<KIND>(ga, R);
+    if (blocks == 0) return 0;
+    ABACUS_CHECK_ARG((int64_t)ga.E * ga.tiles_m * ga.tiles_n < (1ll << 31), "%s: tile grid too large", name);
+    hipLaunchKernelGGL(pipe::gemm_bf16_wgrad_kernel<KIND>, dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
     ABACUS_CHECK_LAUNCH(name);
     return 0;
   }
@@ -1367,7 +1664,7 @@ namespace {
 int check_gemm_shape(int64_t R, int64_t D, int64_t M, int64_t E, int dtype) {
   ABACUS_CHECK_ARG(dtype == kF32 || dtype == kBF16, "unsupported dtype code %d (0 = fp32, 1 = bf16)", dtype);
   const int vec = dtype == kBF16 ? 8 : 4;
-  ABACUS_CHECK_ARG(E >= 1 && E <= 4096, "n_experts %lld out of range", (long long)E);
+  ABACUS_CHECK_ARG(E >= 1 && E <= pipe::kMaxExperts, "n_experts %lld out of range", (long long)E);
   ABACUS_CHECK_ARG(R >= 0 && R < (1ll << 31), "routed rows %lld out of range", (long long)R);
   ABACUS_CHECK_ARG(D >= 1 && D % vec == 0 && D < (1ll << 31), "dim %lld must be a positive multiple of %d",
                    (long long)D, vec);

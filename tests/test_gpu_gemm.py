@@ -207,3 +207,69 @@ def test_row_tiles_every_remainder_class():
         close(dU[a:b], dh * gg * sg, f"dU expert {e}", 2e-2)
         close(dX[a:b], f(o["dgate"][a:b]) @ f(o["w_gate"][e]).T + f(o["dup"][a:b]) @ f(o["w_up"][e]).T,
               f"dX expert {e}")
+
+
+WGRAD_CASES = [
+    # (counts per expert, D, M): fewer tiles than CUs (most blocks find no tile), and more
+    ([5, 0, 300, 64], 256, 256),
+    ([700, 0, 1500, 64, 1030, 0], 1024, 2048),
+]
+
+
+def _wgrads(o, D, M, s, out=None):
+    """Both weight gradients through the single entry points (persistent tile loop), into `out` or new buffers."""
+    E, R = o["E"], o["R"]
+    if out is None:
+        out = tuple(torch.full(shape, float("nan"), dtype=torch.bfloat16, device="cuda")
+                    for shape in ((E, M, D), (E, D, M), (E, D, M)))
+    dwd, dwg, dwu = out
+    call("abacus_moe_down_bwd_wgrad", ptr(o["h"]), ptr(o["dy"]), ptr(o["offsets"]), R, M, D, E, 1, ptr(dwd), s)
+    call("abacus_moe_gateup_bwd_wgrad", ptr(o["xp"]), ptr(o["dgate"]), ptr(o["dup"]), ptr(o["offsets"]), R, D, M, E,
+         1, ptr(dwg), ptr(dwu), s)
+    return out
+
+
+@pytest.mark.parametrize("counts,D,M", WGRAD_CASES, ids=["few_tiles", "many_tiles"])
+def test_wgrad_tile_loop(counts, D, M):
+    """Weight gradients from the persistent tile loop: each expert's product (fp64 truth), exact
+    zeros for experts without rows, bit-identical results over more launches than there are
+    counter slots (each launch's counters must be left at zero), and on two streams at once."""
+    o = _operands(counts, D, M, torch.bfloat16, seed=31)
+    dev = torch.device("cuda")
+    s = _lib.stream_of(dev)
+    first = _wgrads(o, D, M, s)
+    torch.cuda.synchronize()
+    for name, t in zip(("dw_down", "dw_gate", "dw_up"), first):
+        assert not torch.isnan(t).any(), f"{name}: unwritten elements"
+    f = lambda t: t.double().cpu()
+    off = o["offsets"].tolist()
+    for e, c in enumerate(counts):
+        a, b = off[e], off[e + 1]
+        if c == 0:
+            for t in first:
+                assert torch.count_nonzero(t[e]) == 0
+            continue
+        for got, want, name in ((first[0][e], f(o["h"][a:b]).T @ f(o["dy"][a:b]), "dw_down"),
+                                (first[1][e], f(o["xp"][a:b]).T @ f(o["dgate"][a:b]), "dw_gate"),
+                                (first[2][e], f(o["xp"][a:b]).T @ f(o["dup"][a:b]), "dw_up")):
+            err = float((f(got) - want).norm() / want.norm())
+            assert err < 1e-2, f"expert {e} {name}: relative error {err:.3g}"
+    # 70 launches of each kind on one stream (more than the 64 counter slots), same buffers
+    again = tuple(torch.empty_like(t) for t in first)
+    for i in range(70):
+        for t in again:
+            t.fill_(float("nan"))
+        _wgrads(o, D, M, s, again)
+        torch.cuda.synchronize()
+        for a, b, name in zip(first, again, ("dw_down", "dw_gate", "dw_up")):
+            assert torch.equal(a, b), f"launch {i + 1}: {name} differs"
+    # two streams (default priority) with launches in flight on both at once
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    outs = [tuple(torch.full_like(t, float("nan")) for t in first) for _ in range(6)]
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs):
+        _wgrads(o, D, M, streams[i % 2].cuda_stream, out)
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs):
+        for a, b, name in zip(first, out, ("dw_down", "dw_gate", "dw_up")):
+            assert torch.equal(a, b), f"stream launch {i}: {name} differs"
