@@ -21,6 +21,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
 _F = ctypes.c_float
+_D = ctypes.c_double
 
 # name -> (restype, argtypes); must match include/abacus_moe.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -58,6 +59,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
     "abacus_rmsnorm_rope_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P]),
     "abacus_rmsnorm_rope_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
+    "abacus_adamw_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _D, _D, _D, _D, _D, _I, _P]),
 }
 
 _lock = threading.Lock()

@@ -210,17 +210,24 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* _
   }
 }
 
-// dgamma[d] = sum of the block partials in block order: 64 columns per block,
-// its 4 waves taking blocks b = w, w + 4, ..., added in wave order.
+// dgamma[d] = the sum of the block partials in a fixed order: 64 columns per
+// block; wave w takes partial rows b with (b / 8) % 4 == w into 8 accumulators
+// (u = b % 8: eight loads in flight instead of one), adds them pairwise, and
+// the 4 wave sums are added in wave order.
 template <typename T>
 __global__ __launch_bounds__(256) void rmsnorm_dgamma_kernel(const float* __restrict__ partial, int nblocks, int D,
                                                              T* __restrict__ dgamma) {
   __shared__ float s_part[4][64];
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + l;
-  float s = 0.f;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (col < D)
-    for (int b = w; b < nblocks; b += 4) s += partial[(int64_t)b * D + col];
+    for (int b0 = 8 * w; b0 < nblocks; b0 += 32) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (b0 + u < nblocks) a[u] += partial[(int64_t)(b0 + u) * D + col];
+    }
+  const float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
   s_part[w][l] = s;
   __syncthreads();
   if (w == 0 && col < D) dgamma[col] = from_f32<T>(s_part[0][l] + s_part[1][l] + s_part[2][l] + s_part[3][l]);

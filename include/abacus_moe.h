@@ -214,6 +214,23 @@ int abacus_rmsnorm_rope_bwd(const void* dy, const void* x, const void* gamma, co
                             const void* sin_LK, int64_t rows, int64_t L, int64_t H, int64_t K, int dtype, void* dx,
                             void* dgamma, float* ws, int64_t ws_bytes, void* stream);
 
+/* One AdamW step (optimizers/adamw.py:85-119, AdamW.step) over n tensors in
+ * as few launches as possible: for tensor i, params[i], grads[i], exp_avgs[i]
+ * and exp_avg_sqs[i] hold numels[i] contiguous elements of `dtype` (16-byte
+ * aligned device memory), and steps[i] is its step count after this step's
+ * increment.  params, grads, exp_avgs, exp_avg_sqs, numels and steps are host
+ * arrays.  Every element goes through the reference's tensor-op sequence with
+ * a rounding to `dtype` after each op:
+ *   p = p*(1 - lr*wd); m = lerp(m, g, 1 - beta1); v = v*beta2 + (1 - beta2)*(g*g);
+ *   d = sqrt(v) / sqrt(1 - beta2^step) + eps; p = p + (-lr / (1 - beta1^step)) * (m / d)
+ * in fp32, in the forms of torch's device kernels: the lerp, the (1 - beta2)
+ * product and the final update are fused multiply-adds, division by
+ * sqrt(1 - beta2^step) is a product with its reciprocal (taken in double), and
+ * the scalars are the double-precision values rounded to fp32. */
+int abacus_adamw_step(void* const* params, const void* const* grads, void* const* exp_avgs, void* const* exp_avg_sqs,
+                      const int64_t* numels, const int64_t* steps, int n, double lr, double beta1, double beta2,
+                      double eps, double weight_decay, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
