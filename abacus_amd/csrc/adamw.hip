@@ -47,25 +47,79 @@ struct AdamwArgs {
   float eps;
 };
 
+// Rounds x and y to T's precision: bf16 by one v_cvt_pk_bf16_f32 for both
+// (round to nearest even, the same bits as f32_to_bf16); fp32 unchanged.
 template <typename T>
-__device__ inline float rnd(float x) {
-  return round_to<T>(x);
+__device__ inline void rnd2(float& x, float& y);
+template <>
+__device__ inline void rnd2<float>(float&, float&) {}
+template <>
+__device__ inline void rnd2<uint16_t>(float& x, float& y) {
+  const uint32_t w = pack_bf16x2(x, y);
+  x = lo_bf16(w);
+  y = hi_bf16(w);
 }
 
-// One element through the reference's op sequence (fused multiply-adds only
-// where torch's device kernels have them).
+// Two elements through the reference's op sequence, each op's results rounded
+// together (fused multiply-adds only where torch's device kernels have them).
 template <typename T>
-__device__ inline void adamw_elem(float& p, float g, float& m, float& v, const AdamwArgs& a, float nss, float isb) {
+__device__ inline void adamw_pair(float (&p)[2], const float (&g)[2], float (&m)[2], float (&v)[2],
+                                  const AdamwArgs& a, float nss, float isb) {
 #pragma clang fp contract(off)
-  p = rnd<T>(p * a.decay);
-  m = a.w1 < 0.5f ? rnd<T>(__builtin_fmaf(a.w1, g - m, m)) : rnd<T>(g - (g - m) * (1.0f - a.w1));
-  v = rnd<T>(v * a.beta2);
-  v = rnd<T>(__builtin_fmaf(a.a2, g * g, v));
-  float d = rnd<T>(sqrtf(v));  // correctly rounded (hipcc's default); __fsqrt_rn is not, on gfx950
-  d = rnd<T>(d * isb);
-  d = rnd<T>(d + a.eps);
-  p = rnd<T>(__builtin_fmaf(nss, __fdiv_rn(m, d), p));
+  float d[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) p[k] = p[k] * a.decay;
+  rnd2<T>(p[0], p[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    m[k] = a.w1 < 0.5f ? __builtin_fmaf(a.w1, g[k] - m[k], m[k]) : g[k] - (g[k] - m[k]) * (1.0f - a.w1);
+  rnd2<T>(m[0], m[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) v[k] = v[k] * a.beta2;
+  rnd2<T>(v[0], v[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) v[k] = __builtin_fmaf(a.a2, g[k] * g[k], v[k]);
+  rnd2<T>(v[0], v[1]);
+  // sqrtf and / are correctly rounded (hipcc's default); __fsqrt_rn is not, on gfx950
+#pragma unroll
+  for (int k = 0; k < 2; ++k) d[k] = sqrtf(v[k]);
+  rnd2<T>(d[0], d[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) d[k] = d[k] * isb;
+  rnd2<T>(d[0], d[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) d[k] = d[k] + a.eps;
+  rnd2<T>(d[0], d[1]);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) p[k] = __builtin_fmaf(nss, m[k] / d[k], p[k]);
+  rnd2<T>(p[0], p[1]);
 }
+
+// Element pairs of one 16-byte vector: bf16 packs a pair per 32-bit word
+// (values already on the bf16 grid, so packing is exact); fp32 a pair per two.
+template <typename T>
+struct Pairs;
+template <>
+struct Pairs<uint16_t> {
+  static constexpr int N = 4;
+  __device__ static inline void get(const Vec16& x, int k, float (&o)[2]) {
+    o[0] = lo_bf16(x.w[k]);
+    o[1] = hi_bf16(x.w[k]);
+  }
+  __device__ static inline void put(Vec16& x, int k, const float (&o)[2]) { x.w[k] = pack_bf16x2(o[0], o[1]); }
+};
+template <>
+struct Pairs<float> {
+  static constexpr int N = 2;
+  __device__ static inline void get(const Vec16& x, int k, float (&o)[2]) {
+    o[0] = bits_f32(x.w[2 * k]);
+    o[1] = bits_f32(x.w[2 * k + 1]);
+  }
+  __device__ static inline void put(Vec16& x, int k, const float (&o)[2]) {
+    x.w[2 * k] = f32_bits(o[0]);
+    x.w[2 * k + 1] = f32_bits(o[1]);
+  }
+};
 
 // Elements per 16-byte vector and per block.
 template <typename T>
@@ -77,6 +131,7 @@ struct AdamwGeo {
 template <typename T>
 __global__ __launch_bounds__(kAdamwThreads) void adamw_kernel(AdamwArgs a) {
   constexpr int EPV = AdamwGeo<T>::EPV, EPB = AdamwGeo<T>::EPB;
+  using PR = Pairs<T>;
   // this block's tensor (block_start is ascending; n <= kAdamwMaxTensors)
   int i = 0;
   while (i + 1 < a.n && (int)blockIdx.x >= a.block_start[i + 1]) ++i;
@@ -103,33 +158,38 @@ __global__ __launch_bounds__(kAdamwThreads) void adamw_kernel(AdamwArgs a) {
   for (int u = 0; u < kAdamwVecs; ++u) {
     const int64_t e0 = base + ((int64_t)u * kAdamwThreads + threadIdx.x) * EPV;
     if (e0 + EPV <= n) {
-      const T* tp = reinterpret_cast<const T*>(&vp[u]);
-      const T* tg = reinterpret_cast<const T*>(&vg[u]);
-      const T* tm = reinterpret_cast<const T*>(&vm[u]);
-      const T* tv = reinterpret_cast<const T*>(&vv[u]);
       Vec16 op, om, ov;
-      T* wp = reinterpret_cast<T*>(&op);
-      T* wm = reinterpret_cast<T*>(&om);
-      T* wv = reinterpret_cast<T*>(&ov);
 #pragma unroll
-      for (int k = 0; k < EPV; ++k) {
-        float p = to_f32<T>(tp[k]), m = to_f32<T>(tm[k]), v = to_f32<T>(tv[k]);
-        adamw_elem<T>(p, to_f32<T>(tg[k]), m, v, a, nss, isb);
-        wp[k] = from_f32<T>(p);
-        wm[k] = from_f32<T>(m);
-        wv[k] = from_f32<T>(v);
+      for (int k = 0; k < PR::N; ++k) {
+        float p[2], g[2], m[2], v[2];
+        PR::get(vp[u], k, p);
+        PR::get(vg[u], k, g);
+        PR::get(vm[u], k, m);
+        PR::get(vv[u], k, v);
+        adamw_pair<T>(p, g, m, v, a, nss, isb);
+        PR::put(op, k, p);
+        PR::put(om, k, m);
+        PR::put(ov, k, v);
       }
       st16(P + e0, op);
       st16(M + e0, om);
       st16(V + e0, ov);
     } else if (e0 < n) {
-      // the tensor's last, partial vector
-      for (int64_t e = e0; e < n; ++e) {
-        float p = to_f32<T>(P[e]), m = to_f32<T>(M[e]), v = to_f32<T>(V[e]);
-        adamw_elem<T>(p, to_f32<T>(G[e]), m, v, a, nss, isb);
-        P[e] = from_f32<T>(p);
-        M[e] = from_f32<T>(m);
-        V[e] = from_f32<T>(v);
+      // the tensor's last, partial vector, a pair at a time (an odd last element
+      // is paired with a copy of itself that is not stored)
+      for (int64_t e = e0; e < n; e += 2) {
+        const int64_t f = e + 1 < n ? e + 1 : e;
+        float p[2] = {to_f32<T>(P[e]), to_f32<T>(P[f])}, g[2] = {to_f32<T>(G[e]), to_f32<T>(G[f])};
+        float m[2] = {to_f32<T>(M[e]), to_f32<T>(M[f])}, v[2] = {to_f32<T>(V[e]), to_f32<T>(V[f])};
+        adamw_pair<T>(p, g, m, v, a, nss, isb);
+        P[e] = from_f32<T>(p[0]);
+        M[e] = from_f32<T>(m[0]);
+        V[e] = from_f32<T>(v[0]);
+        if (f != e) {
+          P[f] = from_f32<T>(p[1]);
+          M[f] = from_f32<T>(m[1]);
+          V[f] = from_f32<T>(v[1]);
+        }
       }
     }
   }

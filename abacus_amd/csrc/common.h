@@ -35,6 +35,18 @@ template <typename T> __host__ __device__ inline float round_to(float v);
 template <> __host__ __device__ inline float round_to<float>(float v) { return v; }
 template <> __host__ __device__ inline float round_to<uint16_t>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+// Two floats to packed bf16 in one v_cvt_pk_bf16_f32 (gfx950): round to
+// nearest even, NaN made quiet -- bit-identical to f32_to_bf16 for every
+// input; lo_bf16 / hi_bf16 widen the halves back to fp32.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ inline float lo_bf16(uint32_t w) { return bits_f32(w << 16); }
+__device__ inline float hi_bf16(uint32_t w) { return bits_f32(w & 0xffff0000u); }
+
 template <typename T> __host__ __device__ inline float to_f32(T v);
 template <> __host__ __device__ inline float to_f32<float>(float v) { return v; }
 template <> __host__ __device__ inline float to_f32<uint16_t>(uint16_t v) { return bf16_to_f32(v); }

@@ -211,26 +211,40 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* _
 }
 
 // dgamma[d] = the sum of the block partials in a fixed order: 64 columns per
-// block; wave w takes partial rows b with (b / 8) % 4 == w into 8 accumulators
-// (u = b % 8: eight loads in flight instead of one), adds them pairwise, and
-// the 4 wave sums are added in wave order.
+// block; wave w of 16 loads partial rows 16w .. 16w+15 of each 256 at once
+// (the rows come from other XCDs' writes, one memory round trip away) and
+// adds them pairwise; the 16 wave sums are added in wave order.
+constexpr int kDgammaWaves = 16;
 template <typename T>
-__global__ __launch_bounds__(256) void rmsnorm_dgamma_kernel(const float* __restrict__ partial, int nblocks, int D,
-                                                             T* __restrict__ dgamma) {
-  __shared__ float s_part[4][64];
+__global__ __launch_bounds__(kDgammaWaves * 64) void rmsnorm_dgamma_kernel(const float* __restrict__ partial,
+                                                                           int nblocks, int D,
+                                                                           T* __restrict__ dgamma) {
+  __shared__ float s_part[kDgammaWaves][64];
   const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int col = blockIdx.x * 64 + l;
-  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (col < D)
-    for (int b0 = 8 * w; b0 < nblocks; b0 += 32) {
+  float total = 0.f;
+  for (int r0 = 0; r0 < nblocks; r0 += kDgammaWaves * 16) {
+    float a[16];
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (b0 + u < nblocks) a[u] += partial[(int64_t)(b0 + u) * D + col];
+    for (int u = 0; u < 16; ++u) {
+      const int b = r0 + 16 * w + u;
+      a[u] = col < D && b < nblocks ? partial[(int64_t)b * D + col] : 0.f;
     }
-  const float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
-  s_part[w][l] = s;
-  __syncthreads();
-  if (w == 0 && col < D) dgamma[col] = from_f32<T>(s_part[0][l] + s_part[1][l] + s_part[2][l] + s_part[3][l]);
+#pragma unroll
+    for (int h = 8; h >= 1; h >>= 1)
+#pragma unroll
+      for (int u = 0; u < h; ++u) a[u] += a[u + h];
+    s_part[w][l] = a[0];
+    __syncthreads();
+    if (w == 0) {
+      float t = 0.f;
+#pragma unroll
+      for (int v = 0; v < kDgammaWaves; ++v) t += s_part[v][l];
+      total += t;
+    }
+    __syncthreads();
+  }
+  if (w == 0 && col < D) dgamma[col] = from_f32<T>(total);
 }
 
 // Lanes per row: the largest power of two up to 64 dividing the row's vectors.
@@ -315,10 +329,10 @@ int norm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd
   if (rows == 0) {
     // no rows: dgamma is zero
     if (dtype == kBF16)
-      hipLaunchKernelGGL(rmsnorm_dgamma_kernel<uint16_t>, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, s, ws, 0,
+      hipLaunchKernelGGL(rmsnorm_dgamma_kernel<uint16_t>, dim3((unsigned)((D + 63) / 64)), dim3(kDgammaWaves * 64), 0, s, ws, 0,
                          (int)D, (uint16_t*)dgamma);
     else
-      hipLaunchKernelGGL(rmsnorm_dgamma_kernel<float>, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, s, ws, 0,
+      hipLaunchKernelGGL(rmsnorm_dgamma_kernel<float>, dim3((unsigned)((D + 63) / 64)), dim3(kDgammaWaves * 64), 0, s, ws, 0,
                          (int)D, (float*)dgamma);
     ABACUS_CHECK_LAUNCH("rmsnorm_dgamma");
     return 0;
@@ -343,10 +357,10 @@ int norm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd
 #undef ABACUS_NORM_BWD
   ABACUS_CHECK_LAUNCH("rmsnorm_bwd");
   if (dtype == kBF16)
-    hipLaunchKernelGGL(rmsnorm_dgamma_kernel<uint16_t>, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, s, ws, nb,
+    hipLaunchKernelGGL(rmsnorm_dgamma_kernel<uint16_t>, dim3((unsigned)((D + 63) / 64)), dim3(kDgammaWaves * 64), 0, s, ws, nb,
                        (int)D, (uint16_t*)dgamma);
   else
-    hipLaunchKernelGGL(rmsnorm_dgamma_kernel<float>, dim3((unsigned)((D + 63) / 64)), dim3(256), 0, s, ws, nb,
+    hipLaunchKernelGGL(rmsnorm_dgamma_kernel<float>, dim3((unsigned)((D + 63) / 64)), dim3(kDgammaWaves * 64), 0, s, ws, nb,
                        (int)D, (float*)dgamma);
   ABACUS_CHECK_LAUNCH("rmsnorm_dgamma");
   return 0;

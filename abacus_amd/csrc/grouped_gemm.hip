@@ -560,17 +560,6 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
 }
 
-// Two floats to packed bf16 in one v_cvt_pk_bf16_f32: round to nearest even,
-// NaN made quiet -- bit-identical to f32_to_bf16 for every input.
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-__device__ inline uint32_t pack_bf16x2(float a, float b) {
-  const f32x2_t v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
-__device__ inline float lo_bf16(uint32_t w) { return bits_f32(w << 16); }
-__device__ inline float hi_bf16(uint32_t w) { return bits_f32(w & 0xffff0000u); }
-
 // 1 / (1 + exp(-x)) from the hardware exp2 and reciprocal (a few ulp in fp32,
 // far below the bf16 rounding of every value it feeds).  The forward SiLU and
 // its recomputation in the down-projection backward both use it, so the two
