@@ -30,7 +30,10 @@ namespace abacus {
 
 namespace {
 
-constexpr int kNormWaves = 4;
+// Waves per block: 16, or 8 where the backward's per-wave dgamma sums (64
+// lanes x elements per lane, fp32) would pass 128 KB of LDS.  Many waves per
+// CU keep enough row loads in flight to cover the memory latency.
+__host__ __device__ constexpr int norm_waves(int elems_per_lane) { return elems_per_lane <= 32 ? 16 : 8; }
 constexpr int kNormMaxBlocks = 1024;   // forward grid cap
 constexpr int kNormBwdBlocks = 256;    // backward grid cap (one dgamma partial row each)
 
@@ -61,7 +64,7 @@ __device__ inline float row_sum(float v, int lpr) {
 }
 
 template <typename T, int VPL, bool ROPE>
-__global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_fwd_kernel(const T* __restrict__ x,
+__global__ __launch_bounds__(norm_waves(VPL * VecTraits<T>::kN) * 64) void rmsnorm_fwd_kernel(const T* __restrict__ x,
                                                                       const T* __restrict__ gamma, int64_t rows,
                                                                       int D, int lpr, float eps, T* __restrict__ y,
                                                                       float* __restrict__ rstd,
@@ -69,13 +72,14 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_fwd_kernel(const T* _
                                                                       const T* __restrict__ sinv, int L, int H) {
   static_assert(!ROPE || VPL == 1, "the rotary pairs sit on partner lanes");
   constexpr int EPV = VecTraits<T>::kN;
+  constexpr int W = norm_waves(VPL * EPV);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rpw = 64 / lpr, sub = lane / lpr, li = lane % lpr;
   const int64_t groups = (rows + rpw - 1) / rpw;
   Vec16 gv[VPL];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) gv[v] = ld16(gamma + (li + v * lpr) * EPV);
-  for (int64_t g = (int64_t)blockIdx.x * kNormWaves + wave; g < groups; g += (int64_t)gridDim.x * kNormWaves) {
+  for (int64_t g = (int64_t)blockIdx.x * W + wave; g < groups; g += (int64_t)gridDim.x * W) {
     const int64_t r = g * rpw + sub;
     const bool act = r < rows;
     Vec16 xv[VPL];
@@ -124,7 +128,7 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_fwd_kernel(const T* _
 }
 
 template <typename T, int VPL, bool ROPE>
-__global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* __restrict__ dy,
+__global__ __launch_bounds__(norm_waves(VPL * VecTraits<T>::kN) * 64) void rmsnorm_bwd_kernel(const T* __restrict__ dy,
                                                                       const T* __restrict__ x,
                                                                       const T* __restrict__ gamma,
                                                                       const float* __restrict__ rstd, int64_t rows,
@@ -135,7 +139,8 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* _
   static_assert(!ROPE || VPL == 1, "the rotary pairs sit on partner lanes");
   constexpr int EPV = VecTraits<T>::kN;
   constexpr int NE = VPL * EPV;  // elements per lane
-  __shared__ float red_s[kNormWaves][64 * NE];
+  constexpr int W = norm_waves(NE);
+  __shared__ float red_s[W][64 * NE];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rpw = 64 / lpr, sub = lane / lpr, li = lane % lpr;
   const int64_t groups = (rows + rpw - 1) / rpw;
@@ -144,7 +149,7 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* _
   for (int v = 0; v < VPL; ++v) unpack<T>(ld16(gamma + (li + v * lpr) * EPV), gf + v * EPV);
 #pragma unroll
   for (int i = 0; i < NE; ++i) dg[i] = 0.f;
-  for (int64_t g = (int64_t)blockIdx.x * kNormWaves + wave; g < groups; g += (int64_t)gridDim.x * kNormWaves) {
+  for (int64_t g = (int64_t)blockIdx.x * W + wave; g < groups; g += (int64_t)gridDim.x * W) {
     const int64_t r = g * rpw + sub;
     const bool act = r < rows;
     float xf[NE], df[NE];
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(kNormWaves * 64) void rmsnorm_bwd_kernel(const T* _
     const int l = vec % lpr, v = vec / lpr;
     float sum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kNormWaves; ++w) sum += red_s[w][l * NE + v * EPV + e];
+    for (int w = 0; w < W; ++w) sum += red_s[w][l * NE + v * EPV + e];
     partial[(int64_t)blockIdx.x * D + col] = sum;
   }
 }
@@ -288,10 +293,11 @@ int norm_fwd(const void* x, const void* gamma, int64_t rows, int64_t D, float ep
   }
   if (rows == 0) return 0;
   const int64_t groups = norm_groups(rows, lpr);
-  const unsigned grid = (unsigned)std::min<int64_t>(kNormMaxBlocks, (groups + kNormWaves - 1) / kNormWaves);
+  const int W = norm_waves(vpl * (dtype == kBF16 ? 8 : 4));
+  const unsigned grid = (unsigned)std::min<int64_t>(kNormMaxBlocks, (groups + W - 1) / W);
   hipStream_t s = (hipStream_t)stream;
 #define ABACUS_NORM_FWD(TT, V, R)                                                                                 \
-  hipLaunchKernelGGL((rmsnorm_fwd_kernel<TT, V, R>), dim3(grid), dim3(kNormWaves * 64), 0, s, (const TT*)x,       \
+  hipLaunchKernelGGL((rmsnorm_fwd_kernel<TT, V, R>), dim3(grid), dim3(W * 64), 0, s, (const TT*)x,                \
                      (const TT*)gamma, rows, (int)D, lpr, eps, (TT*)y, rstd, (const TT*)cosv, (const TT*)sinv,   \
                      (int)L, (int)H)
   if (dtype == kBF16) {
@@ -323,7 +329,8 @@ int norm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd
   }
   hipStream_t s = (hipStream_t)stream;
   const int64_t groups = norm_groups(rows, lpr);
-  const int nb = (int)std::max<int64_t>(1, std::min<int64_t>(kNormBwdBlocks, (groups + kNormWaves - 1) / kNormWaves));
+  const int W = norm_waves(vpl * (dtype == kBF16 ? 8 : 4));
+  const int nb = (int)std::max<int64_t>(1, std::min<int64_t>(kNormBwdBlocks, (groups + W - 1) / W));
   ABACUS_CHECK_ARG(rows == 0 || ws_bytes >= (int64_t)nb * D * 4, "rmsnorm_bwd: workspace of %lld bytes, need %lld",
                    (long long)ws_bytes, (long long)nb * D * 4);
   if (rows == 0) {
@@ -338,7 +345,7 @@ int norm_bwd(const void* dy, const void* x, const void* gamma, const float* rstd
     return 0;
   }
 #define ABACUS_NORM_BWD(TT, V, R)                                                                                  \
-  hipLaunchKernelGGL((rmsnorm_bwd_kernel<TT, V, R>), dim3(nb), dim3(kNormWaves * 64), 0, s, (const TT*)dy,         \
+  hipLaunchKernelGGL((rmsnorm_bwd_kernel<TT, V, R>), dim3(nb), dim3(W * 64), 0, s, (const TT*)dy,                  \
                      (const TT*)x, (const TT*)gamma, rstd, rows, (int)D, lpr, (TT*)dx, ws, (const TT*)cosv,        \
                      (const TT*)sinv, (int)L, (int)H)
   if (dtype == kBF16) {
