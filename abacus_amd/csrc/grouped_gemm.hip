@@ -1097,7 +1097,6 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   }
 }
 
-
 // ---------------- weight gradients: a persistent tile loop ----------------
 // A weight gradient's tile reduces over one expert's rows only (about 1000 at
 // the Mixtral shape: 16 k-tiles, ~30 us of MFMA work), so a block per tile
