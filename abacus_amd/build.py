@@ -41,8 +41,14 @@ def hipcc() -> str:
     return path
 
 
+# Per-file additions.  attention.hip: MFMA results in VGPRs, not AGPRs -- its
+# score and output accumulators are read and rescaled by VALU code every tile,
+# and accumulators in AGPRs cost a move per element each way.
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

@@ -1,0 +1,265 @@
+// Causal multi-head attention of the MoE decoder, flash style, on gfx950 MFMA.
+//
+// Reference: abacus/attention.py:136-141 materialises scores = q k^T / sqrt(K),
+// masks keys after their query, softmaxes and multiplies by v.  Here the
+// scores never leave the chip: each block owns 128 query rows of one (batch,
+// head) and walks the 64-key tiles up to its last query, keeping a running
+// row max and row sum (online softmax, fp32) and rescaling its fp32 output
+// accumulators as the max grows.  bf16, head_dim 64; q, k, v and o in the
+// projections' (B, L, H, K) layout, so no permuted copies are made.
+//
+// Layouts in registers (v_mfma_f32_32x32x16_bf16, D = A B with lane l giving
+// A[l % 32][8 (l / 32) .. +7] and B[8 (l / 32) .. +7][l % 32], and holding
+// D[8 (q / 4) + 4 (l / 32) + q % 4][l % 32] in its accumulator register q):
+//   S^T = K_tile Q^T: lane l ends up with the scores of query l % 32 against
+//   keys 8g + 4h + 0..3 (g = 0..3, h = l / 32) of each 32-key half, so a row's
+//   statistics need its 32 values and lane l ^ 32's;
+//   O^T = V^T P^T: lane l accumulates output dims 8g + 4h + 0..3 of the same
+//   query, so rescaling a row is one factor per lane.  P^T's operand (8
+//   consecutive keys of the lane's query) is built from the score registers
+//   with one 64-bit exchange between lanes l and l ^ 32.
+#include <type_traits>
+
+#include "common.h"
+
+namespace abacus {
+namespace {
+
+constexpr int kHeadDim = 64;
+constexpr int kQRows = 128;   // query rows per block (4 waves x 32)
+constexpr int kKeys = 64;     // keys per tile
+constexpr int kAttnThreads = 256;
+constexpr int kTileBytes = kKeys * kHeadDim * 2;  // one K or V tile: 8 KB
+constexpr int kStages = 2;  // LDS ring depth (2 measured faster than 3: 32 KB per block, more blocks per CU)
+static_assert(kStages == 2 || kStages == 3, "the ring's waits cover one or two tiles ahead");
+
+typedef __bf16 attn_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float attn_f32x16 __attribute__((ext_vector_type(16)));
+typedef short attn_v4i16 __attribute__((ext_vector_type(4)));
+
+__device__ inline void mfma32(attn_f32x16& acc, const Vec16& a, const Vec16& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(attn_bf16x8, a), __builtin_bit_cast(attn_bf16x8, b),
+                                                acc, 0, 0, 0);
+}
+
+// A K or V tile in LDS: 64 rows (keys) of 8 16-byte chunks (dims), the chunk
+// index XOR-swizzled by row: with m = row / 2, swz = (m % 2) * 4 + (m / 2) % 4.
+// Rows 2 apart land 128 bytes apart in the bank space, so a K fragment read
+// (16 consecutive rows, one chunk) needs the 8 even rows of a block of 16 on 8
+// different chunks (swz is a permutation of 0..7 over them), and a V^T read
+// (rows r..r+3, r a multiple of 4, chunks c..c+3 of 8) needs rows r and r+2
+// on complementary halves of the chunks (swz(r+2) = swz(r) ^ 4).  Both are
+// then free of bank conflicts.
+__device__ inline int tile_swz(int row) { return (((row >> 1) & 1) << 2) | ((row >> 2) & 3); }
+__device__ inline int tile_off(int row, int chunk) { return (row * 8 + (chunk ^ tile_swz(row))) * 16; }
+
+// K fragment (A of S^T): key `row0 + l % 32`, dims 16 c + 8 (l / 32) .. +7.
+__device__ inline Vec16 frag_k(const char* tile, int row0, int c, int lane) {
+  return *reinterpret_cast<const Vec16*>(tile + tile_off(row0 + (lane & 31), 2 * c + (lane >> 5)));
+}
+
+// V^T fragment (A of O^T): dim `d0 + l % 32`, keys 16 c + 8 (l / 32) .. +7,
+// from the row-major (key, dim) tile through the LDS transpose read (lane j of
+// each 16-lane group receives element j % 4 of the reads of lanes 4i + j / 4).
+__device__ inline Vec16 frag_vt(const char* tile, int d0, int c, int lane) {
+  const int grp = lane >> 4, s = lane & 15;
+  const int d = d0 + 16 * (grp & 1) + 4 * (s & 3);
+  const int key = 16 * c + 8 * (grp >> 1) + (s >> 2);
+  const int b = (d & 7) * 2;
+  const attn_v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) attn_v4i16*)(tile + tile_off(key, d >> 3) + b));
+  const attn_v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) attn_v4i16*)(tile + tile_off(key + 4, d >> 3) + b));
+  const uint2 a = __builtin_bit_cast(uint2, lo), b2 = __builtin_bit_cast(uint2, hi);
+  Vec16 v;
+  v.w[0] = a.x;
+  v.w[1] = a.y;
+  v.w[2] = b2.x;
+  v.w[3] = b2.y;
+  return v;
+}
+
+// o = softmax(mask(q k^T * scale)) v for one (batch, head) and 128 queries;
+// lse2 = row max + log2(row sum) of the base-2 scaled scores, per query.
+__global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* __restrict__ q,
+                                                                const uint16_t* __restrict__ k,
+                                                                const uint16_t* __restrict__ v, int L, int H,
+                                                                float scale_log2, uint16_t* __restrict__ o,
+                                                                float* __restrict__ lse2) {
+  __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][K, V]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int nq = L / kQRows;
+  const int qb = nq - 1 - (int)blockIdx.x;  // the longest rows first
+  const int head = blockIdx.y, batch = blockIdx.z;
+  const int64_t row_stride = (int64_t)H * kHeadDim;  // elements between consecutive tokens
+  const int64_t base = ((int64_t)batch * L * H + head) * kHeadDim;
+  const int q0 = qb * kQRows + wave * 32;  // this wave's first query
+  const int my_q = q0 + (lane & 31);
+
+  // Q^T fragments (B of S^T): query my_q, dims 16 c + 8 h .. +7
+  Vec16 qf[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) qf[c] = ld16(q + base + (int64_t)my_q * row_stride + 16 * c + 8 * h);
+
+  // Tile DMA: 512 16-byte chunks per K or V tile, two instructions per thread;
+  // instruction i of wave w writes LDS positions p = (4 i + w) * 64 + lane,
+  // which hold (row p / 8, chunk (p % 8) ^ swizzle(row)) of the tile.
+  int64_t src_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int p = (i * 4 + wave) * 64 + lane, row = p >> 3;
+    src_off[i] = (int64_t)row * row_stride + ((p & 7) ^ tile_swz(row)) * 8;
+  }
+  auto dma_tile = [&](int j, int stage) __attribute__((always_inline)) {
+    const int64_t t0 = base + (int64_t)j * kKeys * row_stride;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      dma16(k + t0 + src_off[i], lds[stage][0] + (i * 4 + wave_u) * 1024);
+      dma16(v + t0 + src_off[i], lds[stage][1] + (i * 4 + wave_u) * 1024);
+    }
+  };
+
+  attn_f32x16 oacc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+  float m_run = -__builtin_inff(), l_run = 0.f;
+
+  // One 64-key tile for this wave: scores, (on diagonal tiles) the causal
+  // mask, online softmax, and the P V product.
+  auto tile_step = [&](const char* kt, const char* vt, int key0, auto diag) __attribute__((always_inline)) {
+    // S^T for the two 32-key halves (raw scores)
+    const attn_f32x16 zero = {};
+    attn_f32x16 s[2];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      s[kh] = zero;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) mfma32(s[kh], frag_k(kt, 32 * kh, c, lane), qf[c]);
+    }
+    // on the wave's diagonal tiles, mask keys after the query
+    if constexpr (decltype(diag)::value) {
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (key0 + 32 * kh + 8 * (r >> 2) + 4 * h + (r & 3) > my_q) s[kh][r] = -__builtin_inff();
+    }
+    // the row max over the tile (raw units)
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kh][r]);
+    // (-inf for a row whose keys in this tile all follow it; the running max is
+    // finite from tile 0 on, as key 0 precedes every query)
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    // Lazy rescale: the running max moves only when a row's max grows by
+    // more than 8 (base 2), so probabilities stay below 2^8 and most tiles
+    // skip rescaling the output accumulators (the wave decides together).
+    const bool grow = mx > m_run + 8.0f;
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[t][r] *= alpha;
+      m_run = m_new;
+    }
+    float rs = 0.f;
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][r], scale_log2, -m_run));
+        s[kh][r] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    l_run += rs;
+    // O^T += V^T P^T over the four 16-key chunks
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int kh = c >> 1, r0 = 8 * (c & 1);
+      const uint32_t a0 = pack_bf16x2(s[kh][r0 + 0], s[kh][r0 + 1]);
+      const uint32_t a1 = pack_bf16x2(s[kh][r0 + 2], s[kh][r0 + 3]);
+      const uint32_t b0 = pack_bf16x2(s[kh][r0 + 4], s[kh][r0 + 5]);
+      const uint32_t b1 = pack_bf16x2(s[kh][r0 + 6], s[kh][r0 + 7]);
+      // lane h = 0 holds keys 0..3 and 8..11 of the chunk and needs 0..7;
+      // lane h = 1 holds 4..7 and 12..15 and needs 8..15
+      const uint32_t x0 = (uint32_t)__shfl_xor((int)(h ? a0 : b0), 32, 64);
+      const uint32_t x1 = (uint32_t)__shfl_xor((int)(h ? a1 : b1), 32, 64);
+      Vec16 pf;
+      pf.w[0] = h ? x0 : a0;
+      pf.w[1] = h ? x1 : a1;
+      pf.w[2] = h ? b0 : x0;
+      pf.w[3] = h ? b1 : x1;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) mfma32(oacc[t], frag_vt(vt, 32 * t, c, lane), pf);
+    }
+  };
+
+  // The ring: tiles 0 .. kStages-2 in flight before the loop; at tile j,
+  // once tile j has landed everywhere (this thread's wait, then the barrier,
+  // after which no wave still reads tile j-1's stage), tile j + kStages-1 is
+  // sent into that stage.
+  constexpr int kAhead = kStages - 1;
+  const int ntiles = (qb * kQRows + kQRows) / kKeys;  // keys 0 .. the block's last query (>= 2)
+#pragma unroll
+  for (int t = 0; t < kAhead; ++t) dma_tile(t, t);
+  for (int j = 0; j < ntiles; ++j) {
+    const int buf = j % kStages;
+    // tiles j+1 .. j+kAhead-1 (4 instructions each) may still be in flight
+    if (kAhead >= 2 && j + 1 < ntiles) wait_vmcnt<(kAhead >= 2 ? 4 : 0)>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (j + kAhead < ntiles) dma_tile(j + kAhead, (j + kAhead) % kStages);
+    const int key0 = j * kKeys;
+    if (key0 + kKeys - 1 > q0) {  // the wave's diagonal tiles (a wave-uniform test)
+      if (key0 <= q0 + 31) tile_step(lds[buf][0], lds[buf][1], key0, std::true_type{});
+    } else {
+      tile_step(lds[buf][0], lds[buf][1], key0, std::false_type{});
+    }
+  }
+  // o = O / l, rounded once to bf16; lse2 for the backward
+  const float inv = 1.0f / l_run;
+  uint16_t* orow = o + base + (int64_t)my_q * row_stride;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = pack_bf16x2(oacc[t][4 * g] * inv, oacc[t][4 * g + 1] * inv);
+      w.y = pack_bf16x2(oacc[t][4 * g + 2] * inv, oacc[t][4 * g + 3] * inv);
+      *reinterpret_cast<uint2*>(orow + 32 * t + 8 * g + 4 * h) = w;
+    }
+  if (h == 0) lse2[((int64_t)batch * H + head) * L + my_q] = m_run + __builtin_amdgcn_logf(l_run);
+}
+
+}  // namespace
+}  // namespace abacus
+
+using namespace abacus;
+
+extern "C" int abacus_attention_fwd(const void* q_BLHK, const void* k_BLHK, const void* v_BLHK, int64_t B, int64_t L,
+                                    int64_t H, int64_t K, float scale, int dtype, void* o_BLHK, float* lse_BHL,
+                                    void* stream) {
+  ABACUS_CHECK_ARG(dtype == kBF16, "attention: bf16 only (dtype code %d)", dtype);
+  ABACUS_CHECK_ARG(K == kHeadDim, "attention: head_dim %lld (this kernel takes %d)", (long long)K, kHeadDim);
+  ABACUS_CHECK_ARG(B >= 1 && H >= 1 && L >= kQRows && L % kQRows == 0 && L <= (1 << 24),
+                   "attention: seq_len %lld must be a positive multiple of %d", (long long)L, kQRows);
+  ABACUS_CHECK_ARG(B * H * L * K < (1ll << 40) && B <= 65535 && H <= 65535, "attention: shape too large");
+  ABACUS_CHECK_ARG(q_BLHK && k_BLHK && v_BLHK && o_BLHK && lse_BHL, "attention: null pointer");
+  ABACUS_CHECK_ARG(((uintptr_t)q_BLHK | (uintptr_t)k_BLHK | (uintptr_t)v_BLHK | (uintptr_t)o_BLHK) % 16 == 0,
+                   "attention: q, k, v, o must be 16-byte aligned");
+  const float scale_log2 = scale * 1.4426950408889634f;  // scores to base 2
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(L / kQRows), (unsigned)H, (unsigned)B), dim3(kAttnThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)q_BLHK, (const uint16_t*)k_BLHK, (const uint16_t*)v_BLHK,
+                     (int)L, (int)H, scale_log2, (uint16_t*)o_BLHK, lse_BHL);
+  ABACUS_CHECK_LAUNCH("attention_fwd");
+  return 0;
+}

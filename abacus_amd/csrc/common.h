@@ -47,6 +47,35 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
 __device__ inline float lo_bf16(uint32_t w) { return bits_f32(w << 16); }
 __device__ inline float hi_bf16(uint32_t w) { return bits_f32(w & 0xffff0000u); }
 
+// global_load_lds_dwordx4 issued through inline asm: the compiler does not
+// model it, so it neither inserts vmcnt(0) before LDS reads of other stages
+// nor before barriers; completion is tracked explicitly with wait_vmcnt<N>().
+// M0 holds the (wave-uniform) LDS destination; lane l's 16 bytes land at
+// M0 + 16 l.
+__device__ inline void dma16(const void* src, char* lds_dst) {
+  const uint32_t lds_addr =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_dst);
+  // M0 is reserved by the compiler: save and restore it around the DMA.
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_addr)
+      : "memory");
+}
+
+// Wait until at most N DMA instructions of this thread are outstanding
+// (vmcnt), without waiting on LDS or export counters.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | (((N >> 4) & 3) << 14));
+}
+
+
 template <typename T> __host__ __device__ inline float to_f32(T v);
 template <> __host__ __device__ inline float to_f32<float>(float v) { return v; }
 template <> __host__ __device__ inline float to_f32<uint16_t>(uint16_t v) { return bf16_to_f32(v); }

@@ -25,6 +25,8 @@ more than one process are not part of this build.
 
 from __future__ import annotations
 
+import math
+
 import torch
 
 from . import _lib
@@ -285,6 +287,22 @@ def _fused_causal_attention(q, k, v):
     return out
 
 
+def _flash_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """abacus_attention_fwd takes contiguous bf16 (B, L, H, 64) q, k, v on the GPU, L a multiple of 128."""
+    return (q.is_cuda and q.dim() == 4 and q.dtype == torch.bfloat16 and q.shape[-1] == 64 and q.shape[1] % 128 == 0
+            and all(t.dtype == q.dtype and t.shape == q.shape and t.is_contiguous() for t in (q, k, v)))
+
+
+def _flash_attention_fwd(q_BLHK: torch.Tensor, k_BLHK: torch.Tensor, v_BLHK: torch.Tensor) -> torch.Tensor:
+    """Causal attention in the (B, L, H, K) layout by the HIP flash kernel (scores kept on chip in fp32)."""
+    B, L, H, K = q_BLHK.shape
+    o = torch.empty_like(q_BLHK)
+    lse = torch.empty(B, H, L, dtype=torch.float32, device=q_BLHK.device)
+    _lib.call("abacus_attention_fwd", _lib.ptr(q_BLHK), _lib.ptr(k_BLHK), _lib.ptr(v_BLHK), B, L, H, K,
+              1.0 / math.sqrt(K), _lib.BF16, _lib.ptr(o), _lib.ptr(lse), _lib.stream_of(q_BLHK.device))
+    return o
+
+
 class MultiHeadAttention(torch.nn.Module):
     """Causal multi-head attention with QK-norm and RoPE (attention.py:67-150).
 
@@ -336,20 +354,12 @@ class MultiHeadAttention(torch.nn.Module):
         self.q_norm = RMSNorm(head_dim, sync_grads=sync_qk)
         self.k_norm = RMSNorm(head_dim, sync_grads=sync_qk)
 
-    def _split_heads(self, x_BLD: torch.Tensor, w_DHK: torch.Tensor, norm=None) -> torch.Tensor:
-        B, L, _ = x_BLD.shape
-        projected = x_BLD @ w_DHK.reshape(self.dim, self.local_heads * self.head_dim)  # (B, L, H*K)
-        heads = projected.view(B, L, self.local_heads, self.head_dim)
-        if norm is not None:  # per (b, l, h) row over K: the same before or after the permute
-            heads = norm(heads)
-        return heads.permute(0, 2, 1, 3)  # (B, H, L, K)
-
     def forward(self, x_BLD: torch.Tensor, rotary: Rotary | None = None) -> torch.Tensor:
         if self.context_parallel or self.world_size > 1:
             _single_process("attention parallelism")
         B, L, _ = x_BLD.shape
         H, K = self.local_heads, self.head_dim
-        v = self._split_heads(x_BLD, self.w_v_DHK)
+        v_heads = (x_BLD @ self.w_v_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
         q_heads = (x_BLD @ self.w_q_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
         k_heads = (x_BLD @ self.w_k_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
         cos = sin = None
@@ -359,13 +369,20 @@ class MultiHeadAttention(torch.nn.Module):
                 and _fused_rope_ok(k_heads, self.k_norm.w_gamma_D, cos, sin)):
             # q/k norm and the rotary embedding in one HIP kernel each
             cos_LK, sin_LK = cos.reshape(L, K), sin.reshape(L, K)
-            q = _RMSNormRopeFunction.apply(q_heads, self.q_norm.w_gamma_D, cos_LK, sin_LK, 1e-5).permute(0, 2, 1, 3)
-            k = _RMSNormRopeFunction.apply(k_heads, self.k_norm.w_gamma_D, cos_LK, sin_LK, 1e-5).permute(0, 2, 1, 3)
+            q_blhk = _RMSNormRopeFunction.apply(q_heads, self.q_norm.w_gamma_D, cos_LK, sin_LK, 1e-5)
+            k_blhk = _RMSNormRopeFunction.apply(k_heads, self.k_norm.w_gamma_D, cos_LK, sin_LK, 1e-5)
+            needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q_blhk, k_blhk, v_heads))
+            if not needs_grad and _flash_ok(q_blhk, k_blhk, v_heads):
+                # no autograd graph: the HIP flash kernel on the (B, L, H, K) layout, no permuted copies
+                out = _flash_attention_fwd(q_blhk, k_blhk, v_heads)
+                return out.reshape(B, L, H * K) @ self.w_o_HKD.reshape(H * K, self.dim)
+            q, k = q_blhk.permute(0, 2, 1, 3), k_blhk.permute(0, 2, 1, 3)
         else:
             q = self.q_norm(q_heads).permute(0, 2, 1, 3)  # (B, H, L, K)
             k = self.k_norm(k_heads).permute(0, 2, 1, 3)
             if rotary is not None:
                 q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        v = v_heads.permute(0, 2, 1, 3)  # (B, H, L, K)
         out = _fused_causal_attention(q, k, v) if q.is_cuda else None  # (B, H, L, K)
         if out is None:
             out = _CausalAttention.apply(

@@ -214,6 +214,17 @@ int abacus_rmsnorm_rope_bwd(const void* dy, const void* x, const void* gamma, co
                             const void* sin_LK, int64_t rows, int64_t L, int64_t H, int64_t K, int dtype, void* dx,
                             void* dgamma, float* ws, int64_t ws_bytes, void* stream);
 
+/* Causal attention forward (attention.py:136-141), flash style: for the
+ * B*H (batch, head) pairs of q, k, v in (B, L, H, K) layout (token rows of
+ * H*K contiguous elements, bf16, K = 64, L a multiple of 128),
+ * o = softmax(mask(q k^T * scale)) v in the same layout, with the scores and
+ * probabilities kept on chip in fp32 (the reference rounds them to the
+ * activation dtype) and o rounded once; lse_BHL (fp32, (B, H, L)) gets each
+ * query's log2-sum-exp2 of its base-2 scaled scores (max + log2(sum)), which
+ * the backward uses to rebuild the probabilities. */
+int abacus_attention_fwd(const void* q_BLHK, const void* k_BLHK, const void* v_BLHK, int64_t B, int64_t L, int64_t H,
+                         int64_t K, float scale, int dtype, void* o_BLHK, float* lse_BHL, void* stream);
+
 /* One AdamW step (optimizers/adamw.py:85-119, AdamW.step) over n tensors in
  * as few launches as possible: for tensor i, params[i], grads[i], exp_avgs[i]
  * and exp_avg_sqs[i] hold numels[i] contiguous elements of `dtype` (16-byte
