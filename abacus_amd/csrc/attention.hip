@@ -79,6 +79,49 @@ __device__ inline Vec16 frag_vt(const char* tile, int d0, int c, int lane) {
   return v;
 }
 
+// MFMA operand of 8 consecutive rows from the score layout.  s holds a 32-row
+// half of a lane's column: rows 8g + 4h + 0..3 (g = 0..3) in registers 4g ..
+// 4g+3.  The operand for 16-row chunk c2 of the half needs rows 8h .. 8h + 7
+// of the chunk: lane h = 0 holds 0..3 and 8..11 of it, lane h = 1 holds 4..7
+// and 12..15, so each sends the pair the other needs (one 64-bit exchange
+// between lanes l and l ^ 32).  Values are rounded to bf16 on the way.
+__device__ inline Vec16 row_chunk_operand(const attn_f32x16& s, int c2, int h) {
+  const int r0 = 8 * c2;
+  const uint32_t a0 = pack_bf16x2(s[r0 + 0], s[r0 + 1]);
+  const uint32_t a1 = pack_bf16x2(s[r0 + 2], s[r0 + 3]);
+  const uint32_t b0 = pack_bf16x2(s[r0 + 4], s[r0 + 5]);
+  const uint32_t b1 = pack_bf16x2(s[r0 + 6], s[r0 + 7]);
+  const uint32_t x0 = (uint32_t)__shfl_xor((int)(h ? a0 : b0), 32, 64);
+  const uint32_t x1 = (uint32_t)__shfl_xor((int)(h ? a1 : b1), 32, 64);
+  Vec16 pf;
+  pf.w[0] = h ? x0 : a0;
+  pf.w[1] = h ? x1 : a1;
+  pf.w[2] = h ? b0 : x0;
+  pf.w[3] = h ? b1 : x1;
+  return pf;
+}
+
+// DMA of one 64-row x 128-byte tile (K, V, Q or dO rows of a (batch, head))
+// into a swizzled LDS tile: two instructions per thread; instruction i of wave
+// w writes LDS positions p = (4 i + w) * 64 + lane, which hold (row p / 8,
+// chunk (p % 8) ^ swz(row)) of the tile.
+struct TileDma {
+  int64_t off[2];
+  int wave_u;
+  __device__ inline void init(int64_t row_stride, int wave, int lane) {
+    wave_u = __builtin_amdgcn_readfirstlane(wave);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int p = (i * 4 + wave) * 64 + lane, row = p >> 3;
+      off[i] = (int64_t)row * row_stride + ((p & 7) ^ tile_swz(row)) * 8;
+    }
+  }
+  __device__ inline void issue(const uint16_t* rows0, char* tile) const {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(rows0 + off[i], tile + (i * 4 + wave_u) * 1024);
+  }
+};
+
 // o = softmax(mask(q k^T * scale)) v for one (batch, head) and 128 queries;
 // lse2 = row max + log2(row sum) of the base-2 scaled scores, per query.
 __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* __restrict__ q,
@@ -88,7 +131,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* 
                                                                 float* __restrict__ lse2) {
   __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][K, V]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int nq = L / kQRows;
   const int qb = nq - 1 - (int)blockIdx.x;  // the longest rows first
   const int head = blockIdx.y, batch = blockIdx.z;
@@ -102,22 +144,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* 
 #pragma unroll
   for (int c = 0; c < 4; ++c) qf[c] = ld16(q + base + (int64_t)my_q * row_stride + 16 * c + 8 * h);
 
-  // Tile DMA: 512 16-byte chunks per K or V tile, two instructions per thread;
-  // instruction i of wave w writes LDS positions p = (4 i + w) * 64 + lane,
-  // which hold (row p / 8, chunk (p % 8) ^ swizzle(row)) of the tile.
-  int64_t src_off[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = (i * 4 + wave) * 64 + lane, row = p >> 3;
-    src_off[i] = (int64_t)row * row_stride + ((p & 7) ^ tile_swz(row)) * 8;
-  }
+  TileDma dma;
+  dma.init(row_stride, wave, lane);
   auto dma_tile = [&](int j, int stage) __attribute__((always_inline)) {
     const int64_t t0 = base + (int64_t)j * kKeys * row_stride;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      dma16(k + t0 + src_off[i], lds[stage][0] + (i * 4 + wave_u) * 1024);
-      dma16(v + t0 + src_off[i], lds[stage][1] + (i * 4 + wave_u) * 1024);
-    }
+    dma.issue(k + t0, lds[stage][0]);
+    dma.issue(v + t0, lds[stage][1]);
   };
 
   attn_f32x16 oacc[2];
@@ -184,20 +216,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* 
     // O^T += V^T P^T over the four 16-key chunks
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int kh = c >> 1, r0 = 8 * (c & 1);
-      const uint32_t a0 = pack_bf16x2(s[kh][r0 + 0], s[kh][r0 + 1]);
-      const uint32_t a1 = pack_bf16x2(s[kh][r0 + 2], s[kh][r0 + 3]);
-      const uint32_t b0 = pack_bf16x2(s[kh][r0 + 4], s[kh][r0 + 5]);
-      const uint32_t b1 = pack_bf16x2(s[kh][r0 + 6], s[kh][r0 + 7]);
-      // lane h = 0 holds keys 0..3 and 8..11 of the chunk and needs 0..7;
-      // lane h = 1 holds 4..7 and 12..15 and needs 8..15
-      const uint32_t x0 = (uint32_t)__shfl_xor((int)(h ? a0 : b0), 32, 64);
-      const uint32_t x1 = (uint32_t)__shfl_xor((int)(h ? a1 : b1), 32, 64);
-      Vec16 pf;
-      pf.w[0] = h ? x0 : a0;
-      pf.w[1] = h ? x1 : a1;
-      pf.w[2] = h ? b0 : x0;
-      pf.w[3] = h ? b1 : x1;
+      const Vec16 pf = row_chunk_operand(s[c >> 1], c & 1, h);
 #pragma unroll
       for (int t = 0; t < 2; ++t) mfma32(oacc[t], frag_vt(vt, 32 * t, c, lane), pf);
     }
@@ -240,6 +259,273 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* 
   if (h == 0) lse2[((int64_t)batch * H + head) * L + my_q] = m_run + __builtin_amdgcn_logf(l_run);
 }
 
+// ---------------------------------------------------------------- backward
+// With z = scale * q k^T (masked), P = softmax(z) and dP = dO v^T, the
+// gradients are dz = P (dP - D) with D = rowsum(dO o), dq = scale dz k,
+// dk = scale dz^T q, dv = P^T dO.  P is rebuilt from the forward's lse2.
+
+// D[b, h, i] = sum over the head dim of dO * o (fp32 from the bf16 values):
+// 8 lanes per (b, l, h) row, 32 rows per block.
+__global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const uint16_t* __restrict__ o,
+                                                           const uint16_t* __restrict__ dout, int64_t rows, int L,
+                                                           int H, float* __restrict__ dvec) {
+  const int64_t r = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int li = threadIdx.x & 7;
+  float acc = 0.f;
+  if (r < rows) {
+    const Vec16 a = ld16(o + r * kHeadDim + li * 8), b = ld16(dout + r * kHeadDim + li * 8);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) acc += lo_bf16(a.w[w]) * lo_bf16(b.w[w]) + hi_bf16(a.w[w]) * hi_bf16(b.w[w]);
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 4, 64);
+  if (li == 0 && r < rows) {
+    const int64_t b = r / ((int64_t)L * H), l = (r / H) % L, hh = r % H;
+    dvec[(b * H + hh) * L + l] = acc;
+  }
+}
+
+// dq for 128 queries of one (batch, head), over the key tiles up to the
+// block's last query: the forward's tile walk, with the scores' layout
+// (lane l: its query's scores against keys 8g + 4h + 0..3 of each half)
+// shared by S^T = K Q^T and dP^T = V dO^T, and dq^T += K^T dz^T.
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ dvec, int L, int H,
+    float scale_log2, float scale, uint16_t* __restrict__ dq) {
+  __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][K, V]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
+  const int nq = L / kQRows;
+  const int qb = nq - 1 - (int)blockIdx.x;  // the longest rows first
+  const int head = blockIdx.y, batch = blockIdx.z;
+  const int64_t row_stride = (int64_t)H * kHeadDim;
+  const int64_t base = ((int64_t)batch * L * H + head) * kHeadDim;
+  const int q0 = qb * kQRows + wave * 32;
+  const int my_q = q0 + (lane & 31);
+  const int64_t stat = ((int64_t)batch * H + head) * L + my_q;
+  const float my_lse = lse2[stat], my_d = dvec[stat];
+
+  Vec16 qf[4], df[4];  // B operands: q and dO of my_q, dims 16 c + 8 h .. +7
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    qf[c] = ld16(q + base + (int64_t)my_q * row_stride + 16 * c + 8 * h);
+    df[c] = ld16(dout + base + (int64_t)my_q * row_stride + 16 * c + 8 * h);
+  }
+  TileDma dma;
+  dma.init(row_stride, wave, lane);
+  auto dma_tile = [&](int j, int stage) __attribute__((always_inline)) {
+    const int64_t t0 = base + (int64_t)j * kKeys * row_stride;
+    dma.issue(k + t0, lds[stage][0]);
+    dma.issue(v + t0, lds[stage][1]);
+  };
+  attn_f32x16 dqacc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dqacc[t][r] = 0.f;
+
+  auto tile_step = [&](const char* kt, const char* vt, int key0, auto diag) __attribute__((always_inline)) {
+    const attn_f32x16 zero = {};
+    attn_f32x16 sc[2], dp[2];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+      sc[kh] = zero;
+      dp[kh] = zero;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        mfma32(sc[kh], frag_k(kt, 32 * kh, c, lane), qf[c]);
+        mfma32(dp[kh], frag_k(vt, 32 * kh, c, lane), df[c]);
+      }
+    }
+    // dz = P (dP - D), P = 0 for keys after the query
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kh][r], scale_log2, -my_lse));
+        if constexpr (decltype(diag)::value) {
+          if (key0 + 32 * kh + 8 * (r >> 2) + 4 * h + (r & 3) > my_q) p = 0.f;
+        }
+        sc[kh][r] = p * (dp[kh][r] - my_d);
+      }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const Vec16 zf = row_chunk_operand(sc[c >> 1], c & 1, h);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) mfma32(dqacc[t], frag_vt(kt, 32 * t, c, lane), zf);
+    }
+  };
+
+  constexpr int kAhead = kStages - 1;
+  const int ntiles = (qb * kQRows + kQRows) / kKeys;
+#pragma unroll
+  for (int t = 0; t < kAhead; ++t) dma_tile(t, t);
+  for (int j = 0; j < ntiles; ++j) {
+    const int buf = j % kStages;
+    if (kAhead >= 2 && j + 1 < ntiles) wait_vmcnt<(kAhead >= 2 ? 4 : 0)>();
+    else wait_vmcnt<0>();
+    __syncthreads();
+    if (j + kAhead < ntiles) dma_tile(j + kAhead, (j + kAhead) % kStages);
+    const int key0 = j * kKeys;
+    if (key0 + kKeys - 1 > q0) {
+      if (key0 <= q0 + 31) tile_step(lds[buf][0], lds[buf][1], key0, std::true_type{});
+    } else {
+      tile_step(lds[buf][0], lds[buf][1], key0, std::false_type{});
+    }
+  }
+  uint16_t* row = dq + base + (int64_t)my_q * row_stride;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = pack_bf16x2(dqacc[t][4 * g] * scale, dqacc[t][4 * g + 1] * scale);
+      w.y = pack_bf16x2(dqacc[t][4 * g + 2] * scale, dqacc[t][4 * g + 3] * scale);
+      *reinterpret_cast<uint2*>(row + 32 * t + 8 * g + 4 * h) = w;
+    }
+}
+
+// dk and dv for 128 keys of one (batch, head), over the 64-query tiles from
+// the block's first key to the end.  Each wave keeps k and v of its 32 keys
+// in registers; the scores are formed as S = Q K^T so that lane l holds its
+// key's column against queries 8g + 4h + 0..3 of each 32-query half (the
+// same register layout as the forward's, rows and columns exchanged), and
+// dv^T += dO^T P, dk^T += q^T dz take P and dz as operands through the same
+// lane exchange.  The query tile's lse2 and D values come through LDS.
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ dvec, int L, int H,
+    float scale_log2, float scale, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv) {
+  __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][Q, dO]
+  __shared__ __attribute__((aligned(16))) float stats[kStages][2][kKeys];    // [stage][lse2, D]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
+  const int kb = blockIdx.x;  // key block: the first ones see the most queries
+  const int head = blockIdx.y, batch = blockIdx.z;
+  const int64_t row_stride = (int64_t)H * kHeadDim;
+  const int64_t base = ((int64_t)batch * L * H + head) * kHeadDim;
+  const int64_t stat0 = ((int64_t)batch * H + head) * L;
+  const int k0 = kb * kQRows + wave * 32;  // this wave's first key
+  const int my_k = k0 + (lane & 31);
+
+  Vec16 kf[4], vf[4];  // B operands: k and v of my_k, dims 16 c + 8 h .. +7
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    kf[c] = ld16(k + base + (int64_t)my_k * row_stride + 16 * c + 8 * h);
+    vf[c] = ld16(v + base + (int64_t)my_k * row_stride + 16 * c + 8 * h);
+  }
+  TileDma dma;
+  dma.init(row_stride, wave, lane);
+  const int qt0 = kb * kQRows / kKeys;  // the first query tile that sees these keys
+  auto fetch_tile = [&](int j, int stage) __attribute__((always_inline)) {
+    const int qs = (qt0 + j) * kKeys;
+    const int64_t t0 = base + (int64_t)qs * row_stride;
+    dma.issue(q + t0, lds[stage][0]);
+    dma.issue(dout + t0, lds[stage][1]);
+  };
+  // the tile's 64 lse2 and 64 D values: 32 threads, one float4 each
+  auto load_stats = [&](int j, float4& out) __attribute__((always_inline)) {
+    const int qs = (qt0 + j) * kKeys;
+    if (tid < 32) out = *reinterpret_cast<const float4*>((tid < 16 ? lse2 : dvec) + stat0 + qs + 4 * (tid & 15));
+  };
+  auto store_stats = [&](int stage, const float4& val) __attribute__((always_inline)) {
+    if (tid < 32) *reinterpret_cast<float4*>(&stats[stage][tid >> 4][4 * (tid & 15)]) = val;
+  };
+  attn_f32x16 dkacc[2], dvacc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dkacc[t][r] = 0.f;
+      dvacc[t][r] = 0.f;
+    }
+
+  auto tile_step = [&](const char* qt, const char* dt, const float* lse_s, const float* d_s, int qs,
+                       auto diag) __attribute__((always_inline)) {
+    const attn_f32x16 zero = {};
+#pragma unroll
+    for (int qh = 0; qh < 2; ++qh) {
+      attn_f32x16 sc = zero, dp = zero;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        mfma32(sc, frag_k(qt, 32 * qh, c, lane), kf[c]);
+        mfma32(dp, frag_k(dt, 32 * qh, c, lane), vf[c]);
+      }
+      attn_f32x16 pz;  // P, then sc becomes dz
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int qi = 32 * qh + 8 * g + 4 * h;  // query index in the tile of registers 4g .. 4g+3
+        const float4 l4 = *reinterpret_cast<const float4*>(lse_s + qi);
+        const float4 d4 = *reinterpret_cast<const float4*>(d_s + qi);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dvv[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r], scale_log2, -lv[e]));
+          if constexpr (decltype(diag)::value) {
+            if (qs + qi + e < my_k) p = 0.f;
+          }
+          pz[r] = p;
+          sc[r] = p * (dp[r] - dvv[e]);
+        }
+      }
+#pragma unroll
+      for (int c2 = 0; c2 < 2; ++c2) {
+        const int c = 2 * qh + c2;  // 16-query chunk of the tile
+        const Vec16 pf = row_chunk_operand(pz, c2, h);
+        const Vec16 zf = row_chunk_operand(sc, c2, h);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          mfma32(dvacc[t], frag_vt(dt, 32 * t, c, lane), pf);
+          mfma32(dkacc[t], frag_vt(qt, 32 * t, c, lane), zf);
+        }
+      }
+    }
+  };
+
+  constexpr int kAhead = kStages - 1;
+  static_assert(kAhead == 1, "the stats are staged one tile ahead");
+  const int ntiles = L / kKeys - qt0;
+  {
+    float4 st0 = make_float4(0.f, 0.f, 0.f, 0.f);
+    fetch_tile(0, 0);
+    load_stats(0, st0);
+    store_stats(0, st0);
+  }
+  for (int j = 0; j < ntiles; ++j) {
+    const int buf = j % kStages;
+    wait_vmcnt<0>();
+    __syncthreads();
+    float4 st = make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool more = j + 1 < ntiles;
+    if (more) {
+      fetch_tile(j + 1, (j + 1) % kStages);
+      load_stats(j + 1, st);
+    }
+    const int qs = (qt0 + j) * kKeys;
+    if (qs < k0 + 31) {  // some query of the tile precedes some key of the wave
+      if (qs + kKeys - 1 >= k0) tile_step(lds[buf][0], lds[buf][1], stats[buf][0], stats[buf][1], qs, std::true_type{});
+    } else {
+      tile_step(lds[buf][0], lds[buf][1], stats[buf][0], stats[buf][1], qs, std::false_type{});
+    }
+    if (more) store_stats((j + 1) % kStages, st);
+  }
+  uint16_t* krow = dk + base + (int64_t)my_k * row_stride;
+  uint16_t* vrow = dv + base + (int64_t)my_k * row_stride;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      uint2 w;
+      w.x = pack_bf16x2(dkacc[t][4 * g] * scale, dkacc[t][4 * g + 1] * scale);
+      w.y = pack_bf16x2(dkacc[t][4 * g + 2] * scale, dkacc[t][4 * g + 3] * scale);
+      *reinterpret_cast<uint2*>(krow + 32 * t + 8 * g + 4 * h) = w;
+      w.x = pack_bf16x2(dvacc[t][4 * g], dvacc[t][4 * g + 1]);
+      w.y = pack_bf16x2(dvacc[t][4 * g + 2], dvacc[t][4 * g + 3]);
+      *reinterpret_cast<uint2*>(vrow + 32 * t + 8 * g + 4 * h) = w;
+    }
+}
+
 }  // namespace
 }  // namespace abacus
 
@@ -261,5 +547,42 @@ extern "C" int abacus_attention_fwd(const void* q_BLHK, const void* k_BLHK, cons
                      (hipStream_t)stream, (const uint16_t*)q_BLHK, (const uint16_t*)k_BLHK, (const uint16_t*)v_BLHK,
                      (int)L, (int)H, scale_log2, (uint16_t*)o_BLHK, lse_BHL);
   ABACUS_CHECK_LAUNCH("attention_fwd");
+  return 0;
+}
+
+extern "C" int64_t abacus_attention_bwd_ws_bytes(int64_t B, int64_t L, int64_t H) { return B * H * L * 4; }
+
+extern "C" int abacus_attention_bwd(const void* q_BLHK, const void* k_BLHK, const void* v_BLHK, const void* o_BLHK,
+                                    const void* dout_BLHK, const float* lse_BHL, int64_t B, int64_t L, int64_t H,
+                                    int64_t K, float scale, int dtype, void* dq_BLHK, void* dk_BLHK, void* dv_BLHK,
+                                    float* ws, int64_t ws_bytes, void* stream) {
+  ABACUS_CHECK_ARG(dtype == kBF16, "attention: bf16 only (dtype code %d)", dtype);
+  ABACUS_CHECK_ARG(K == kHeadDim, "attention: head_dim %lld (this kernel takes %d)", (long long)K, kHeadDim);
+  ABACUS_CHECK_ARG(B >= 1 && H >= 1 && L >= kQRows && L % kQRows == 0 && L <= (1 << 24),
+                   "attention: seq_len %lld must be a positive multiple of %d", (long long)L, kQRows);
+  ABACUS_CHECK_ARG(B * H * L * K < (1ll << 40) && B <= 65535 && H <= 65535, "attention: shape too large");
+  ABACUS_CHECK_ARG(q_BLHK && k_BLHK && v_BLHK && o_BLHK && dout_BLHK && lse_BHL && dq_BLHK && dk_BLHK && dv_BLHK && ws,
+                   "attention: null pointer");
+  ABACUS_CHECK_ARG(((uintptr_t)q_BLHK | (uintptr_t)k_BLHK | (uintptr_t)v_BLHK | (uintptr_t)o_BLHK |
+                    (uintptr_t)dout_BLHK | (uintptr_t)dq_BLHK | (uintptr_t)dk_BLHK | (uintptr_t)dv_BLHK |
+                    (uintptr_t)lse_BHL | (uintptr_t)ws) % 16 == 0,
+                   "attention: tensors must be 16-byte aligned");
+  ABACUS_CHECK_ARG(ws_bytes >= B * H * L * 4, "attention_bwd: workspace of %lld bytes, need %lld",
+                   (long long)ws_bytes, (long long)(B * H * L * 4));
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t rows = B * L * H;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(attn_bwd_dot_kernel, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s,
+                     (const uint16_t*)o_BLHK, (const uint16_t*)dout_BLHK, rows, (int)L, (int)H, ws);
+  ABACUS_CHECK_LAUNCH("attention_bwd (dot)");
+  const dim3 grid((unsigned)(L / kQRows), (unsigned)H, (unsigned)B);
+  hipLaunchKernelGGL(attn_bwd_dkdv_kernel, grid, dim3(kAttnThreads), 0, s, (const uint16_t*)q_BLHK,
+                     (const uint16_t*)k_BLHK, (const uint16_t*)v_BLHK, (const uint16_t*)dout_BLHK, lse_BHL, ws,
+                     (int)L, (int)H, scale_log2, scale, (uint16_t*)dk_BLHK, (uint16_t*)dv_BLHK);
+  ABACUS_CHECK_LAUNCH("attention_bwd (dk, dv)");
+  hipLaunchKernelGGL(attn_bwd_dq_kernel, grid, dim3(kAttnThreads), 0, s, (const uint16_t*)q_BLHK,
+                     (const uint16_t*)k_BLHK, (const uint16_t*)v_BLHK, (const uint16_t*)dout_BLHK, lse_BHL, ws,
+                     (int)L, (int)H, scale_log2, scale, (uint16_t*)dq_BLHK);
+  ABACUS_CHECK_LAUNCH("attention_bwd (dq)");
   return 0;
 }

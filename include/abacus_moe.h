@@ -225,6 +225,21 @@ int abacus_rmsnorm_rope_bwd(const void* dy, const void* x, const void* gamma, co
 int abacus_attention_fwd(const void* q_BLHK, const void* k_BLHK, const void* v_BLHK, int64_t B, int64_t L, int64_t H,
                          int64_t K, float scale, int dtype, void* o_BLHK, float* lse_BHL, void* stream);
 
+/* Bytes of fp32 workspace abacus_attention_bwd needs (one value per query). */
+int64_t abacus_attention_bwd_ws_bytes(int64_t B, int64_t L, int64_t H);
+
+/* Causal attention backward: the gradients of abacus_attention_fwd's o with
+ * respect to q, k and v (what autograd derives for attention.py:136-141), from
+ * q, k, v, the forward's o and lse_BHL, and dout = dL/do, all in the forward's
+ * layouts and restrictions.  Probabilities are rebuilt from lse_BHL in fp32;
+ * with D = rowsum(dout * o), dz = P (dout v^T - D), dq = scale dz k,
+ * dk = scale dz^T q, dv = P^T dout, each rounded once to bf16.  ws: device
+ * workspace of abacus_attention_bwd_ws_bytes bytes (16-byte aligned). */
+int abacus_attention_bwd(const void* q_BLHK, const void* k_BLHK, const void* v_BLHK, const void* o_BLHK,
+                         const void* dout_BLHK, const float* lse_BHL, int64_t B, int64_t L, int64_t H, int64_t K,
+                         float scale, int dtype, void* dq_BLHK, void* dk_BLHK, void* dv_BLHK, float* ws,
+                         int64_t ws_bytes, void* stream);
+
 /* One AdamW step (optimizers/adamw.py:85-119, AdamW.step) over n tensors in
  * as few launches as possible: for tensor i, params[i], grads[i], exp_avgs[i]
  * and exp_avg_sqs[i] hold numels[i] contiguous elements of `dtype` (16-byte
