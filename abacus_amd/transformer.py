@@ -293,14 +293,41 @@ def _flash_ok(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
             and all(t.dtype == q.dtype and t.shape == q.shape and t.is_contiguous() for t in (q, k, v)))
 
 
-def _flash_attention_fwd(q_BLHK: torch.Tensor, k_BLHK: torch.Tensor, v_BLHK: torch.Tensor) -> torch.Tensor:
-    """Causal attention in the (B, L, H, K) layout by the HIP flash kernel (scores kept on chip in fp32)."""
-    B, L, H, K = q_BLHK.shape
-    o = torch.empty_like(q_BLHK)
-    lse = torch.empty(B, H, L, dtype=torch.float32, device=q_BLHK.device)
-    _lib.call("abacus_attention_fwd", _lib.ptr(q_BLHK), _lib.ptr(k_BLHK), _lib.ptr(v_BLHK), B, L, H, K,
-              1.0 / math.sqrt(K), _lib.BF16, _lib.ptr(o), _lib.ptr(lse), _lib.stream_of(q_BLHK.device))
-    return o
+class _FlashAttentionFunction(torch.autograd.Function):
+    """Causal attention (attention.py:136-141) in the (B, L, H, K) layout by the HIP flash kernels.
+
+    The forward keeps scores and probabilities on chip in fp32 and saves each
+    query's log2-sum-exp2; the backward rebuilds the probabilities from it and
+    forms dq, dk, dv without materialising an (L, L) matrix.
+    """
+
+    @staticmethod
+    def forward(ctx, q_BLHK, k_BLHK, v_BLHK):
+        B, L, H, K = q_BLHK.shape
+        o = torch.empty_like(q_BLHK)
+        lse = torch.empty(B, H, L, dtype=torch.float32, device=q_BLHK.device)
+        _lib.call("abacus_attention_fwd", _lib.ptr(q_BLHK), _lib.ptr(k_BLHK), _lib.ptr(v_BLHK), B, L, H, K,
+                  1.0 / math.sqrt(K), _lib.BF16, _lib.ptr(o), _lib.ptr(lse), _lib.stream_of(q_BLHK.device))
+        ctx.save_for_backward(q_BLHK, k_BLHK, v_BLHK, o, lse)
+        return o
+
+    @staticmethod
+    def backward(ctx, d_o):
+        q, k, v, o, lse = ctx.saved_tensors
+        B, L, H, K = q.shape
+        d_o = d_o.contiguous()
+        dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+        nbytes = _lib.query("abacus_attention_bwd_ws_bytes", B, L, H)
+        ws = torch.empty(nbytes // 4, dtype=torch.float32, device=q.device)
+        _lib.call("abacus_attention_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(d_o),
+                  _lib.ptr(lse), B, L, H, K, 1.0 / math.sqrt(K), _lib.BF16, _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+                  _lib.ptr(ws), nbytes, _lib.stream_of(q.device))
+        return dq, dk, dv
+
+
+# The HIP flash kernels take the attention whenever _flash_ok holds; False
+# sends it to torch's fused kernels (as for every other shape).
+flash_attention_enabled = True
 
 
 class MultiHeadAttention(torch.nn.Module):
@@ -371,10 +398,9 @@ class MultiHeadAttention(torch.nn.Module):
             cos_LK, sin_LK = cos.reshape(L, K), sin.reshape(L, K)
             q_blhk = _RMSNormRopeFunction.apply(q_heads, self.q_norm.w_gamma_D, cos_LK, sin_LK, 1e-5)
             k_blhk = _RMSNormRopeFunction.apply(k_heads, self.k_norm.w_gamma_D, cos_LK, sin_LK, 1e-5)
-            needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q_blhk, k_blhk, v_heads))
-            if not needs_grad and _flash_ok(q_blhk, k_blhk, v_heads):
-                # no autograd graph: the HIP flash kernel on the (B, L, H, K) layout, no permuted copies
-                out = _flash_attention_fwd(q_blhk, k_blhk, v_heads)
+            if flash_attention_enabled and _flash_ok(q_blhk, k_blhk, v_heads):
+                # the HIP flash kernels on the (B, L, H, K) layout: no permuted copies
+                out = _FlashAttentionFunction.apply(q_blhk, k_blhk, v_heads)
                 return out.reshape(B, L, H * K) @ self.w_o_HKD.reshape(H * K, self.dim)
             q, k = q_blhk.permute(0, 2, 1, 3), k_blhk.permute(0, 2, 1, 3)
         else:

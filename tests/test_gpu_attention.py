@@ -111,9 +111,10 @@ def test_attention_fwd_rejects_shapes():
                   *([_lib.ptr(q)] * 3), _lib.ptr(lse), 16, _lib.stream_of(q.device))
 
 
-def test_attention_module_uses_flash_kernel_without_grad():
-    """MultiHeadAttention under no_grad runs abacus_attention_fwd on the (B, L, H, K) layout and
-    agrees with the gradient-recording path (torch's fused kernel) to bf16 accuracy."""
+def test_attention_module_runs_flash_kernels_forward_and_backward(monkeypatch):
+    """MultiHeadAttention runs abacus_attention_fwd and _bwd on the (B, L, H, K) layout, with
+    and without autograd, and its output and every gradient agree with the same module on
+    torch's fused attention to bf16 accuracy."""
     import copy
 
     from abacus_amd import transformer as tr
@@ -122,11 +123,29 @@ def test_attention_module_uses_flash_kernel_without_grad():
     attn = tr.MultiHeadAttention(H * K, H, K).to(torch.bfloat16).cuda()
     rot = copy.deepcopy(tr.Rotary(K)).to(torch.bfloat16).cuda()
     x = torch.randn(B, L, H * K, device="cuda").to(torch.bfloat16)
+    dy = torch.randn(B, L, H * K, device="cuda").to(torch.bfloat16)
+
+    def run():
+        xi = x.clone().requires_grad_()
+        attn.zero_grad(set_to_none=True)
+        y = attn(xi, rot)
+        y.backward(dy)
+        return [y.detach().float(), xi.grad.float()] + [p.grad.float() for p in attn.parameters()]
+
     timer = _lib.KernelTimer()
-    with timer, torch.no_grad():
-        fast = attn(x, rot)
+    with timer:
+        fast = run()
+        with torch.no_grad():
+            fast_ng = attn(x, rot)
     calls = timer.totals_ms()
-    assert "abacus_attention_fwd" in calls, sorted(calls)
-    slow = attn(x.clone().requires_grad_(), rot)  # records a graph: torch's fused kernel
-    err = float((fast.float() - slow.detach().float()).norm() / slow.detach().float().norm())
-    assert err < 1e-2, err
+    assert "abacus_attention_fwd" in calls and "abacus_attention_bwd" in calls, sorted(calls)
+    monkeypatch.setattr(tr, "flash_attention_enabled", False)
+    timer = _lib.KernelTimer()
+    with timer:
+        slow = run()
+    assert "abacus_attention_fwd" not in timer.totals_ms()
+    names = ["out", "dx"] + [n for n, _ in attn.named_parameters()]
+    for name, a, b in zip(names, fast, slow):
+        err = float((a - b).norm() / b.norm())
+        assert err < 1e-2, f"{name}: {err:.3g}"
+    assert torch.equal(fast_ng.float(), fast[0])
