@@ -330,6 +330,48 @@ class _FlashAttentionFunction(torch.autograd.Function):
 flash_attention_enabled = True
 
 
+class _QKVProjection(torch.autograd.Function):
+    """q, k, v = x W_q, x W_k, x W_v (attention.py:129-131) with one backward for the three.
+
+    The forward runs the three products, each output contiguous as the
+    kernels after it want. The backward concatenates dq, dk, dv once and
+    forms dx = [dq dk dv] [W_q W_k W_v]^T and [dW_q dW_k dW_v] = x^T [dq dk dv]
+    as two GEMMs over the joint width: at T = 8192, D = H*K = 1024 in bf16
+    that takes 157 us against 249 us for three weight-gradient GEMMs (their
+    1024-wide outputs leave hipBLASLt a single round of small tiles), three
+    data-gradient GEMMs and two adds.
+    """
+
+    @staticmethod
+    def forward(ctx, x_BLD, w_q_DHK, w_k_DHK, w_v_DHK):
+        B, L, D = x_BLD.shape
+        _, H, K = w_q_DHK.shape
+        x_TD = x_BLD.reshape(B * L, D)
+        outs = [(x_TD @ w.reshape(D, H * K)).view(B, L, H, K) for w in (w_q_DHK, w_k_DHK, w_v_DHK)]
+        ctx.save_for_backward(x_TD, w_q_DHK, w_k_DHK, w_v_DHK)
+        ctx.x_shape = (B, L, D)
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        x_TD, w_q, w_k, w_v = ctx.saved_tensors
+        B, L, D = ctx.x_shape
+        _, H, K = w_q.shape
+        HK = H * K
+        grads = [torch.zeros(B, L, H, K, dtype=x_TD.dtype, device=x_TD.device) if g is None else g
+                 for g in (dq, dk, dv)]
+        g_T3 = torch.cat([g.reshape(B * L, HK) for g in grads], dim=1)  # (T, 3HK)
+        dx = dwq = dwk = dwv = None
+        if ctx.needs_input_grad[0]:
+            w_D3 = torch.cat([w.reshape(D, HK) for w in (w_q, w_k, w_v)], dim=1)
+            dx = (g_T3 @ w_D3.t()).view(B, L, D)
+        if any(ctx.needs_input_grad[1:]):
+            dw_D3 = x_TD.t() @ g_T3
+            dwq, dwk, dwv = (dw_D3[:, i * HK:(i + 1) * HK].contiguous().view(D, H, K) if ctx.needs_input_grad[1 + i]
+                             else None for i in range(3))
+        return dx, dwq, dwk, dwv
+
+
 class MultiHeadAttention(torch.nn.Module):
     """Causal multi-head attention with QK-norm and RoPE (attention.py:67-150).
 
@@ -386,9 +428,7 @@ class MultiHeadAttention(torch.nn.Module):
             _single_process("attention parallelism")
         B, L, _ = x_BLD.shape
         H, K = self.local_heads, self.head_dim
-        v_heads = (x_BLD @ self.w_v_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
-        q_heads = (x_BLD @ self.w_q_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
-        k_heads = (x_BLD @ self.w_k_DHK.reshape(self.dim, H * K)).view(B, L, H, K)
+        q_heads, k_heads, v_heads = _QKVProjection.apply(x_BLD, self.w_q_DHK, self.w_k_DHK, self.w_v_DHK)
         cos = sin = None
         if rotary is not None:
             cos, sin = rotary(q_heads, seq_dim=1)  # (1, 1, L, K)
