@@ -122,17 +122,23 @@ struct TileDma {
   }
 };
 
-// o = softmax(mask(q k^T * scale)) v for one (batch, head) and 128 queries;
-// lse2 = row max + log2(row sum) of the base-2 scaled scores, per query.
-__global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* __restrict__ q,
-                                                                const uint16_t* __restrict__ k,
-                                                                const uint16_t* __restrict__ v, int L, int H,
-                                                                float scale_log2, uint16_t* __restrict__ o,
-                                                                float* __restrict__ lse2) {
-  __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][K, V]
+// The causal walks give query block qb (2 qb + 2 key tiles) and key block kb
+// (L / 64 - 2 kb query tiles) work in proportion to their place in the
+// sequence.  One work-group takes the pair p and nq-1-p (the middle block
+// alone when nq is odd), so every work-group carries the same work; with one
+// block per work-group the launch ran 1.3x longer than its average share
+// (92.7 against 72.1 us for the forward at B4 L2048 H16).
+typedef char AttnRing[kStages][2][kTileBytes];
+
+// o = softmax(mask(q k^T * scale)) v for one (batch, head) and query block qb
+// (128 queries); lse2 = row max + log2(row sum) of the base-2 scaled scores.
+__device__ __attribute__((always_inline)) inline void attn_fwd_block(const uint16_t* __restrict__ q,
+                                                                    const uint16_t* __restrict__ k,
+                                                                    const uint16_t* __restrict__ v, int L, int H,
+                                                                    float scale_log2, uint16_t* __restrict__ o,
+                                                                    float* __restrict__ lse2, int qb,
+                                                                    AttnRing& lds) {  // [stage][K, V]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
-  const int nq = L / kQRows;
-  const int qb = nq - 1 - (int)blockIdx.x;  // the longest rows first
   const int head = blockIdx.y, batch = blockIdx.z;
   const int64_t row_stride = (int64_t)H * kHeadDim;  // elements between consecutive tokens
   const int64_t base = ((int64_t)batch * L * H + head) * kHeadDim;
@@ -259,6 +265,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* 
   if (h == 0) lse2[((int64_t)batch * H + head) * L + my_q] = m_run + __builtin_amdgcn_logf(l_run);
 }
 
+__global__ __launch_bounds__(kAttnThreads) void attn_fwd_kernel(const uint16_t* __restrict__ q,
+                                                                const uint16_t* __restrict__ k,
+                                                                const uint16_t* __restrict__ v, int L, int H,
+                                                                float scale_log2, uint16_t* __restrict__ o,
+                                                                float* __restrict__ lse2) {
+  __shared__ __attribute__((aligned(1024))) AttnRing lds;
+  const int nq = L / kQRows, p = blockIdx.x;
+  attn_fwd_block(q, k, v, L, H, scale_log2, o, lse2, nq - 1 - p, lds);
+  if (p != nq - 1 - p) {
+    __syncthreads();  // every wave is done with the ring
+    attn_fwd_block(q, k, v, L, H, scale_log2, o, lse2, p, lds);
+  }
+}
+
 // ---------------------------------------------------------------- backward
 // With z = scale * q k^T (masked), P = softmax(z) and dP = dO v^T, the
 // gradients are dz = P (dP - D) with D = rowsum(dO o), dq = scale dz k,
@@ -290,14 +310,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dot_kernel(const uint16_t* __res
 // block's last query: the forward's tile walk, with the scores' layout
 // (lane l: its query's scores against keys 8g + 4h + 0..3 of each half)
 // shared by S^T = K Q^T and dP^T = V dO^T, and dq^T += K^T dz^T.
-__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
+__device__ __attribute__((always_inline)) inline void attn_bwd_dq_block(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ dvec, int L, int H,
-    float scale_log2, float scale, uint16_t* __restrict__ dq) {
-  __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][K, V]
+    float scale_log2, float scale, uint16_t* __restrict__ dq, int qb, AttnRing& lds) {  // [stage][K, V]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
-  const int nq = L / kQRows;
-  const int qb = nq - 1 - (int)blockIdx.x;  // the longest rows first
   const int head = blockIdx.y, batch = blockIdx.z;
   const int64_t row_stride = (int64_t)H * kHeadDim;
   const int64_t base = ((int64_t)batch * L * H + head) * kHeadDim;
@@ -386,6 +403,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
     }
 }
 
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ dvec, int L, int H,
+    float scale_log2, float scale, uint16_t* __restrict__ dq) {
+  __shared__ __attribute__((aligned(1024))) AttnRing lds;
+  const int nq = L / kQRows, p = blockIdx.x;
+  attn_bwd_dq_block(q, k, v, dout, lse2, dvec, L, H, scale_log2, scale, dq, nq - 1 - p, lds);
+  if (p != nq - 1 - p) {
+    __syncthreads();
+    attn_bwd_dq_block(q, k, v, dout, lse2, dvec, L, H, scale_log2, scale, dq, p, lds);
+  }
+}
+
 // dk and dv for 128 keys of one (batch, head), over the 64-query tiles from
 // the block's first key to the end.  Each wave keeps k and v of its 32 keys
 // in registers; the scores are formed as S = Q K^T so that lane l holds its
@@ -393,14 +423,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dq_kernel(
 // same register layout as the forward's, rows and columns exchanged), and
 // dv^T += dO^T P, dk^T += q^T dz take P and dz as operands through the same
 // lane exchange.  The query tile's lse2 and D values come through LDS.
-__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
+typedef float AttnStats[kStages][2][kKeys];
+
+__device__ __attribute__((always_inline)) inline void attn_bwd_dkdv_block(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ dvec, int L, int H,
-    float scale_log2, float scale, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv) {
-  __shared__ __attribute__((aligned(1024))) char lds[kStages][2][kTileBytes];  // [stage][Q, dO]
-  __shared__ __attribute__((aligned(16))) float stats[kStages][2][kKeys];    // [stage][lse2, D]
+    float scale_log2, float scale, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int kb,
+    AttnRing& lds, AttnStats& stats) {  // [stage][Q, dO], [stage][lse2, D]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
-  const int kb = blockIdx.x;  // key block: the first ones see the most queries
   const int head = blockIdx.y, batch = blockIdx.z;
   const int64_t row_stride = (int64_t)H * kHeadDim;
   const int64_t base = ((int64_t)batch * L * H + head) * kHeadDim;
@@ -526,6 +556,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
     }
 }
 
+__global__ __launch_bounds__(kAttnThreads) void attn_bwd_dkdv_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dout, const float* __restrict__ lse2, const float* __restrict__ dvec, int L, int H,
+    float scale_log2, float scale, uint16_t* __restrict__ dk, uint16_t* __restrict__ dv) {
+  __shared__ __attribute__((aligned(1024))) AttnRing lds;
+  __shared__ __attribute__((aligned(16))) AttnStats stats;
+  const int nk = L / kQRows, p = blockIdx.x;
+  attn_bwd_dkdv_block(q, k, v, dout, lse2, dvec, L, H, scale_log2, scale, dk, dv, p, lds, stats);
+  if (p != nk - 1 - p) {
+    __syncthreads();
+    attn_bwd_dkdv_block(q, k, v, dout, lse2, dvec, L, H, scale_log2, scale, dk, dv, nk - 1 - p, lds, stats);
+  }
+}
+
 }  // namespace
 }  // namespace abacus
 
@@ -543,7 +587,8 @@ extern "C" int abacus_attention_fwd(const void* q_BLHK, const void* k_BLHK, cons
   ABACUS_CHECK_ARG(((uintptr_t)q_BLHK | (uintptr_t)k_BLHK | (uintptr_t)v_BLHK | (uintptr_t)o_BLHK) % 16 == 0,
                    "attention: q, k, v, o must be 16-byte aligned");
   const float scale_log2 = scale * 1.4426950408889634f;  // scores to base 2
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(L / kQRows), (unsigned)H, (unsigned)B), dim3(kAttnThreads), 0,
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)((L / kQRows + 1) / 2), (unsigned)H, (unsigned)B),
+                     dim3(kAttnThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)q_BLHK, (const uint16_t*)k_BLHK, (const uint16_t*)v_BLHK,
                      (int)L, (int)H, scale_log2, (uint16_t*)o_BLHK, lse_BHL);
   ABACUS_CHECK_LAUNCH("attention_fwd");
@@ -575,7 +620,7 @@ extern "C" int abacus_attention_bwd(const void* q_BLHK, const void* k_BLHK, cons
   hipLaunchKernelGGL(attn_bwd_dot_kernel, dim3((unsigned)((rows + 31) / 32)), dim3(256), 0, s,
                      (const uint16_t*)o_BLHK, (const uint16_t*)dout_BLHK, rows, (int)L, (int)H, ws);
   ABACUS_CHECK_LAUNCH("attention_bwd (dot)");
-  const dim3 grid((unsigned)(L / kQRows), (unsigned)H, (unsigned)B);
+  const dim3 grid((unsigned)((L / kQRows + 1) / 2), (unsigned)H, (unsigned)B);  // block pairs
   hipLaunchKernelGGL(attn_bwd_dkdv_kernel, grid, dim3(kAttnThreads), 0, s, (const uint16_t*)q_BLHK,
                      (const uint16_t*)k_BLHK, (const uint16_t*)v_BLHK, (const uint16_t*)dout_BLHK, lse_BHL, ws,
                      (int)L, (int)H, scale_log2, scale, (uint16_t*)dk_BLHK, (uint16_t*)dv_BLHK);
