@@ -477,6 +477,11 @@ __global__ __launch_bounds__(WM* WN * 64, MINB) void grouped_gemm_kernel(GemmArg
 // transpose read) are free of bank conflicts.  A transposed read gives each
 // lane 4 consecutive k of one column; two of them form the 8-k MFMA operand.
 // ===========================================================================
+// Split tail: at most kSplitParts slices per tail tile; the reduce pass takes
+// kSplitReduceRows rows of a tile per block.
+constexpr int kSplitParts = 3;
+constexpr int kSplitReduceRows = 16;
+
 namespace pipe {
 
 #ifndef ABACUS_PIPE_BK
@@ -1368,7 +1373,9 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, Gemm
 
 // Adds the slices of each split tail tile in slice order and writes the tile
 // (kinds whose epilogue is a plain store of the bf16-rounded product).  Block
-// i serves tail tile i.
+// (i, j) serves rows kSplitReduceRows j .. +kSplitReduceRows-1 of tail tile i:
+// the tail is fewer tiles than CUs, and one block per tile left the pass
+// latency-bound on a few CUs.
 template <int KIND>
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   using KT = KindTraits<KIND>;
@@ -1386,17 +1393,24 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   if (!find_row_tile<BM>(g, tl.mt, e, row0, row_end)) return;
   const float* ws = g.split_ws + (int64_t)blockIdx.x * g.split_parts * (BM * BN);
   constexpr int CV = BN / 8;
-  for (int v = threadIdx.x; v < BM * CV; v += 256) {
-    const int r = v / CV, c = (v % CV) * 8;
+  for (int v = threadIdx.x; v < kSplitReduceRows * CV; v += 256) {
+    const int r = (int)blockIdx.y * kSplitReduceRows + v / CV, c = (v % CV) * 8;
     const int row = row0 + r, col = n0 + c;
     if (row >= row_end || col >= g.Ndim) continue;
+    float4 lo[kSplitParts], hi[kSplitParts];
+#pragma unroll
+    for (int p = 0; p < kSplitParts; ++p)
+      if (p < S) {
+        lo[p] = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c);
+        hi[p] = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c + 4);
+      }
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int p = 0; p < S; ++p) {
-      const float4 lo = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c);
-      const float4 hi = *reinterpret_cast<const float4*>(ws + (int64_t)p * (BM * BN) + r * BN + c + 4);
-      s[0] += lo.x; s[1] += lo.y; s[2] += lo.z; s[3] += lo.w;
-      s[4] += hi.x; s[5] += hi.y; s[6] += hi.z; s[7] += hi.w;
-    }
+#pragma unroll
+    for (int p = 0; p < kSplitParts; ++p)
+      if (p < S) {
+        s[0] += lo[p].x; s[1] += lo[p].y; s[2] += lo[p].z; s[3] += lo[p].w;
+        s[4] += hi[p].x; s[5] += hi[p].y; s[6] += hi[p].z; s[7] += hi[p].w;
+      }
     Vec16 out;
 #pragma unroll
     for (int w = 0; w < 4; ++w) out.w[w] = pack_bf16x2(s[2 * w], s[2 * w + 1]);
@@ -1546,7 +1560,6 @@ inline int cu_count() {
 // count; the host sizes the grid for any count up to its upper bound: the
 // whole-tile blocks for the largest multiple of the CU count the bound
 // allows, and kSplitParts slices of fewer than CU-count tail tiles.
-constexpr int kSplitParts = 3;
 struct SplitPlan {
   int whole_blocks = 0, slice_blocks = 0, tail_max = 0;
   bool on() const { return slice_blocks > 0; }
@@ -1578,7 +1591,8 @@ int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws
   if (launch_rows<KIND, -1>(ga, R, nullptr, (int64_t)plan.whole_blocks + plan.slice_blocks, false, s, name))
     return 1;
   ga.thin = 0;
-  hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail_max), dim3(256), 0, s, ga);
+  hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail_max, pipe::BM / kSplitReduceRows), dim3(256),
+                     0, s, ga);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
