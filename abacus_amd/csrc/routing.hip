@@ -13,6 +13,8 @@
 // from the saved logits.
 #include <algorithm>
 
+#include <climits>
+
 #include "common.h"
 
 namespace abacus {
@@ -95,7 +97,29 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   const T* xrow = x + (int64_t)(row_ok ? row : 0) * D;
   const int kg = (lane >> 4) * VEC;
   const bool vec_ok = (D % VEC) == 0;  // rows are 16-byte aligned only then
-  for (int kb = wave * KB; kb < D; kb += 4 * KB) {
+  // U k-blocks per batch, all their loads in flight before their MFMAs: one
+  // k-block at a time left the pass waiting out a memory latency per k-block.
+  constexpr int U = NF <= 2 ? 8 : 4;
+  int kb0 = wave * KB;
+  if (vec_ok) {
+    for (; kb0 + (U - 1) * 4 * KB < D; kb0 += U * 4 * KB) {
+      Vec16 a[U], b[U][NF];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int k = kb0 + u * 4 * KB + kg;
+        const bool k_ok = k < D;
+        a[u] = (row_ok && k_ok) ? ld16(xrow + k) : zero16();
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+          b[u][f] = k_ok ? ld16(wt + (int64_t)(f * 16 + (lane & 15)) * D + k) : zero16();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a[u], b[u][f]);
+    }
+  }
+  for (int kb = kb0; kb < D; kb += 4 * KB) {
     const int k = kb + kg;
     Vec16 a, b[NF];
     if (vec_ok) {
@@ -321,6 +345,43 @@ __device__ inline void sort_slots_by_expert(int K, int* e, int* p, float* w) {
   }
 }
 
+// Token t's K slots ordered by expert, read by every lane of a wave (the same
+// cache line): expert e, dispatched row p, coefficient w = coef(k).  A fixed
+// compare-exchange network keeps the arrays in registers; slots k >= K get
+// e = INT_MAX and sort last.  Exchanges only on a strictly greater expert, so
+// the order is the insertion sort's.
+template <typename Coef>
+__device__ __attribute__((always_inline)) inline void token_slots_by_expert(int t, int K,
+                                                                           const int32_t* __restrict__ idx,
+                                                                           const int32_t* __restrict__ pos,
+                                                                           Coef coef, int* e, int* p, float* w) {
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {
+    const bool on = k < K;
+    e[k] = on ? idx[(int64_t)t * K + k] : INT_MAX;
+    p[k] = on && pos ? pos[(int64_t)t * K + k] : 0;
+    w[k] = on ? coef((int64_t)t * K + k) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < kMaxK - 1; ++i)
+#pragma unroll
+    for (int j = 0; j < kMaxK - 1 - i; ++j)
+      if (e[j] > e[j + 1]) {
+        const int te = e[j], tp = p[j];
+        const float tw = w[j];
+        e[j] = e[j + 1];
+        p[j] = p[j + 1];
+        w[j] = w[j + 1];
+        e[j + 1] = te;
+        p[j + 1] = tp;
+        w[j + 1] = tw;
+      }
+}
+
+// Row vectors per lane whose loads of one slot are in flight together in the
+// wave-per-token gather kernels.
+constexpr int kGatherBatch = 4;
+
 // ---------------------------------------------------------------------------
 // K6: combine.  out[t] = sum_k round(y[pos(t,k)] * w(t,k)), experts ascending,
 // fp32 accumulation, one rounding (the stack().sum(0) of moe.py:85).
@@ -331,43 +392,47 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ 
                                                           const int32_t* __restrict__ idx,
                                                           const int32_t* __restrict__ pos, int T_, int D, int K,
                                                           T* __restrict__ out) {
+  // one token per wave: no barrier between the slot reads and the row reads,
+  // and kGatherBatch row vectors of a slot in flight per lane
   constexpr int VEC = VecTraits<T>::kN;
-  __shared__ int s_p[kMaxK];
-  __shared__ float s_w[kMaxK];
-  const int tid = threadIdx.x;
+  constexpr int U = kGatherBatch;
+  const int lane = threadIdx.x & 63;
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= T_) return;
+  int e[kMaxK], p[kMaxK];
+  float w[kMaxK];
+  token_slots_by_expert(t, K, idx, pos, [&](int64_t i) { return to_f32<T>(weights[i]); }, e, p, w);
   const int nvec = D / VEC;
-  for (int t = blockIdx.x; t < T_; t += gridDim.x) {
-    if (tid == 0) {
-      int e[kMaxK], p[kMaxK];
-      float w[kMaxK];
-      for (int k = 0; k < K; ++k) {
-        e[k] = idx[(int64_t)t * K + k];
-        p[k] = pos[(int64_t)t * K + k];
-        w[k] = to_f32<T>(weights[(int64_t)t * K + k]);
+  for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
+    float acc[U][VEC];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[u][i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      if (k >= K) break;
+      Vec16 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        v[u] = c < nvec ? ld16(y + (int64_t)p[k] * D + c * VEC) : zero16();
       }
-      sort_slots_by_expert(K, e, p, w);
-      for (int k = 0; k < K; ++k) {
-        s_p[k] = p[k];
-        s_w[k] = w[k];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[u][i] += round_to<T>(VecTraits<T>::get(v[u], i) * w[k]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * 64 + lane;
+      if (c < nvec) {
+        Vec16 o;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) VecTraits<T>::set(o, i, acc[u][i]);
+        st16(out + (int64_t)t * D + c * VEC, o);
       }
     }
-    __syncthreads();
-    for (int c = tid; c < nvec; c += 256) {
-      float acc[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
-      for (int k = 0; k < K; ++k) {
-        const Vec16 v = ld16(y + (int64_t)s_p[k] * D + c * VEC);
-        const float w = s_w[k];
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[i] += round_to<T>(VecTraits<T>::get(v, i) * w);
-      }
-      Vec16 o;
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) VecTraits<T>::set(o, i, acc[i]);
-      st16(out + (int64_t)t * D + c * VEC, o);
-    }
-    __syncthreads();
   }
 }
 
@@ -545,6 +610,65 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const T* __restrict_
       st16(dx + (int64_t)t * D + c * VEC, o);
     }
     __syncthreads();
+  }
+}
+
+// The same per-token sum for 16-byte-aligned rows, one token per wave, as
+// combine_fwd_kernel: no barrier between the slot reads and the row reads,
+// kGatherBatch row vectors of a slot in flight per lane.  The sum per element
+// is the block kernel's, in the same order.
+template <typename T>
+__global__ __launch_bounds__(256) void unpermute_bwd_wave_kernel(const T* __restrict__ dxp,
+                                                                 const float* __restrict__ dlogit,
+                                                                 const int32_t* __restrict__ idx,
+                                                                 const int32_t* __restrict__ pos,
+                                                                 const T* __restrict__ wt, int T_, int D, int K,
+                                                                 T* __restrict__ dx) {
+  constexpr int VEC = VecTraits<T>::kN;
+  constexpr int U = kGatherBatch;
+  const int lane = threadIdx.x & 63;
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= T_) return;
+  int e[kMaxK], p[kMaxK];
+  float dl[kMaxK];
+  token_slots_by_expert(t, K, idx, dxp ? pos : nullptr, [&](int64_t i) { return dlogit[i]; }, e, p, dl);
+  const int nvec = D / VEC;
+  for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
+    float acc[U][VEC];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) acc[u][i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxK; ++k) {
+      if (k >= K) break;
+      Vec16 xv[U], wv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        xv[u] = (dxp && c < nvec) ? ld16(dxp + (int64_t)p[k] * D + c * VEC) : zero16();
+        wv[u] = c < nvec ? ld16(wt + (int64_t)e[k] * D + c * VEC) : zero16();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (dxp) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[u][i] += VecTraits<T>::get(xv[u], i);
+        }
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) acc[u][i] += dl[k] * VecTraits<T>::get(wv[u], i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * 64 + lane;
+      if (c < nvec) {
+        Vec16 o;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) VecTraits<T>::set(o, i, acc[u][i]);
+        st16(dx + (int64_t)t * D + c * VEC, o);
+      }
+    }
   }
 }
 
@@ -891,7 +1015,8 @@ int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32
   if (check_route_shape(T, D, K, K, dtype)) return 1;
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
-  const int grid = (int)std::min<int64_t>(T, 1 << 20);
+  ABACUS_CHECK_ARG(T <= (int64_t)INT_MAX - 3, "too many tokens (%lld)", (long long)T);
+  const unsigned grid = (unsigned)((T + 3) / 4);  // a token per wave
   if (dtype == kBF16)
     hipLaunchKernelGGL(combine_fwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)y_RD,
                        (const uint16_t*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (uint16_t*)out_TD);
@@ -949,6 +1074,18 @@ int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, con
   if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
   else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
   ABACUS_CHECK_LAUNCH("router weight transpose");
+  if (D % (dtype == kBF16 ? 8 : 4) == 0 && T <= (int64_t)INT_MAX - 3) {
+    const unsigned wgrid = (unsigned)((T + 3) / 4);
+    if (dtype == kBF16)
+      hipLaunchKernelGGL(unpermute_bwd_wave_kernel<uint16_t>, dim3(wgrid), dim3(256), 0, s,
+                         (const uint16_t*)dx_perm_RD, dlogit_TK, idx_TK, pos_TK, (const uint16_t*)wt_ws, (int)T,
+                         (int)D, (int)K, (uint16_t*)dx_TD);
+    else
+      hipLaunchKernelGGL(unpermute_bwd_wave_kernel<float>, dim3(wgrid), dim3(256), 0, s, (const float*)dx_perm_RD,
+                         dlogit_TK, idx_TK, pos_TK, (const float*)wt_ws, (int)T, (int)D, (int)K, (float*)dx_TD);
+    ABACUS_CHECK_LAUNCH("unpermute_bwd");
+    return 0;
+  }
   const int grid = (int)std::min<int64_t>(T, 1 << 20);
   if (dtype == kBF16)
     hipLaunchKernelGGL(unpermute_bwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)dx_perm_RD,
