@@ -63,6 +63,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_attention_bwd_ws_bytes": (_I64, [_I64, _I64, _I64]),
     "abacus_attention_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _I64,
                                   _P]),
+    "abacus_cross_entropy_fwd": (_I, [_P, _P, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "abacus_cross_entropy_bwd": (_I, [_P, _P, _P, _P, _F, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_adamw_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _D, _D, _D, _D, _D, _I, _P]),
 }
 

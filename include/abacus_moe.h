@@ -240,6 +240,23 @@ int abacus_attention_bwd(const void* q_BLHK, const void* k_BLHK, const void* v_B
                          float scale, int dtype, void* dq_BLHK, void* dk_BLHK, void* dv_BLHK, float* ws,
                          int64_t ws_bytes, void* stream);
 
+/* Cross-entropy of the decoder's logits (kernels/liger.py:12-47, called at
+ * trainer.py:81-85), forward: for the N rows of logits_NV ((N, V), `dtype`)
+ * with int64 targets_N, lse_N[i] = log(sum_j exp(x_ij)) and
+ * loss_N[i] = lse_N[i] - x_i[t_i] in fp32, loss_N[i] = 0 where t_i equals
+ * ignore_index (or lies outside [0, V)).  The mean loss is
+ * sum(loss_N) / (number of rows not ignored), as the reference's reduction. */
+int abacus_cross_entropy_fwd(const void* logits_NV, const int64_t* targets_N, int64_t N, int64_t V,
+                             int64_t ignore_index, int dtype, float* lse_N, float* loss_N, void* stream);
+
+/* Cross-entropy backward: dlogits_NV[i][j] = g * scale * (exp(x_ij - lse_N[i])
+ * - [j == t_i]) with g = grad_loss[0] (device memory, fp32) and scale
+ * 1 / (rows not ignored) for the mean; rows whose target is ignored get 0.
+ * Rounded once to `dtype`. */
+int abacus_cross_entropy_bwd(const void* logits_NV, const int64_t* targets_N, const float* lse_N,
+                             const float* grad_loss, float scale, int64_t N, int64_t V, int64_t ignore_index,
+                             int dtype, void* dlogits_NV, void* stream);
+
 /* One AdamW step (optimizers/adamw.py:85-119, AdamW.step) over n tensors in
  * as few launches as possible: for tensor i, params[i], grads[i], exp_avgs[i]
  * and exp_avg_sqs[i] hold numels[i] contiguous elements of `dtype` (16-byte

@@ -36,3 +36,9 @@ def test_no_targets_raises():
     tokens[:, 0] = 1  # only the first position, which is never a target
     with pytest.raises(ValueError, match="no target tokens"):
         next_token_loss(torch.zeros(2, 5, 4), tokens)
+
+
+def test_out_of_range_target_raises():
+    tokens = torch.tensor([[1, 2, 7, 3]])
+    with pytest.raises(IndexError, match="out of bounds"):
+        next_token_loss(torch.zeros(1, 4, 5), tokens)
