@@ -128,6 +128,29 @@ struct AdamwGeo {
   static constexpr int EPB = kAdamwThreads * kAdamwVecs * EPV;
 };
 
+// Nontemporal 16-byte loads and stores: every byte is touched once per step,
+// so keeping it out of the caches' working set helps the stream (3.19 ->
+// 3.00 ms per step over the decoder's 1.2 G bf16 parameters; nontemporal
+// stores alone made no difference).
+typedef unsigned int adamw_u32x4 __attribute__((ext_vector_type(4)));
+__device__ inline Vec16 ld16_stream(const void* p) {
+  const adamw_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const adamw_u32x4*>(p));
+  Vec16 r;
+  r.w[0] = v.x;
+  r.w[1] = v.y;
+  r.w[2] = v.z;
+  r.w[3] = v.w;
+  return r;
+}
+__device__ inline void st16_stream(void* p, const Vec16& x) {
+  adamw_u32x4 v;
+  v.x = x.w[0];
+  v.y = x.w[1];
+  v.z = x.w[2];
+  v.w = x.w[3];
+  __builtin_nontemporal_store(v, reinterpret_cast<adamw_u32x4*>(p));
+}
+
 template <typename T>
 __global__ __launch_bounds__(kAdamwThreads) void adamw_kernel(AdamwArgs a) {
   constexpr int EPV = AdamwGeo<T>::EPV, EPB = AdamwGeo<T>::EPB;
@@ -148,10 +171,10 @@ __global__ __launch_bounds__(kAdamwThreads) void adamw_kernel(AdamwArgs a) {
   for (int u = 0; u < kAdamwVecs; ++u) {
     const int64_t e0 = base + ((int64_t)u * kAdamwThreads + threadIdx.x) * EPV;
     if (e0 + EPV <= n) {
-      vp[u] = ld16(P + e0);
-      vg[u] = ld16(G + e0);
-      vm[u] = ld16(M + e0);
-      vv[u] = ld16(V + e0);
+      vp[u] = ld16_stream(P + e0);
+      vg[u] = ld16_stream(G + e0);
+      vm[u] = ld16_stream(M + e0);
+      vv[u] = ld16_stream(V + e0);
     }
   }
 #pragma unroll
@@ -171,9 +194,9 @@ __global__ __launch_bounds__(kAdamwThreads) void adamw_kernel(AdamwArgs a) {
         PR::put(om, k, m);
         PR::put(ov, k, v);
       }
-      st16(P + e0, op);
-      st16(M + e0, om);
-      st16(V + e0, ov);
+      st16_stream(P + e0, op);
+      st16_stream(M + e0, om);
+      st16_stream(V + e0, ov);
     } else if (e0 < n) {
       // the tensor's last, partial vector, a pair at a time (an odd last element
       // is paired with a copy of itself that is not stored)
