@@ -8,7 +8,8 @@
 //             (running max and rescaled sum, base 2), loss_i = lse_i - x_i[t_i]
 //             (0 for ignored rows)
 //   backward  one pass: dx_ij = g * scale * (exp(x_ij - lse_i) - [j == t_i]),
-//             0 on ignored rows, rounded once to the logits' dtype; g is read
+//             0 on ignored rows, rounded once to the logits' dtype (bf16 pairs by
+//             one hardware conversion, round to nearest even); g is read
 //             from device memory (the loss's incoming gradient), so nothing
 //             waits on the host.
 // A row is one wave's: no barriers, and each lane keeps kCeBatch 16-byte
@@ -22,11 +23,54 @@ namespace abacus {
 
 namespace {
 
-constexpr int kCeBatch = 4;        // vectors per lane in flight
+constexpr int kCeBatch = 4;        // vectors per lane in flight (8 was slower backward)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Logits are read once per pass: nontemporal loads and stores keep them out
+// of the caches' working set.
+typedef unsigned int ce_u32x4 __attribute__((ext_vector_type(4)));
+__device__ inline Vec16 ld16_stream(const void* p) {
+  const ce_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const ce_u32x4*>(p));
+  Vec16 r;
+  r.w[0] = v.x;
+  r.w[1] = v.y;
+  r.w[2] = v.z;
+  r.w[3] = v.w;
+  return r;
+}
+__device__ inline void st16_stream(void* p, const Vec16& x) {
+  ce_u32x4 v;
+  v.x = x.w[0];
+  v.y = x.w[1];
+  v.z = x.w[2];
+  v.w = x.w[3];
+  __builtin_nontemporal_store(v, reinterpret_cast<ce_u32x4*>(p));
+}
+
+// g * exp2(x * log2e - l2) for the 8 bf16 / 4 fp32 elements of a vector,
+// stored in the logits' dtype (bf16 pairs by one hardware conversion).
+template <typename T> struct CeVec;
+template <> struct CeVec<uint16_t> {
+  __device__ static inline Vec16 grad(const Vec16& v, float l2, float gs) {
+    Vec16 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o.w[k] = pack_bf16x2(gs * exp2_fast(__builtin_fmaf(lo_bf16(v.w[k]), kLog2e, -l2)),
+                           gs * exp2_fast(__builtin_fmaf(hi_bf16(v.w[k]), kLog2e, -l2)));
+    return o;
+  }
+};
+template <> struct CeVec<float> {
+  __device__ static inline Vec16 grad(const Vec16& v, float l2, float gs) {
+    Vec16 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o.w[k] = f32_bits(gs * exp2_fast(__builtin_fmaf(bits_f32(v.w[k]), kLog2e, -l2)));
+    return o;
+  }
+};
 
 // (m, s): running max (base-2 scaled units) and sum of exp2(y - m); merge o.
 __device__ inline void lse_merge(float& m, float& s, float om, float os) {
@@ -53,32 +97,32 @@ __global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ x, co
 #pragma unroll
       for (int u = 0; u < kCeBatch; ++u) {
         const int64_t c = c0 + u * 64 + lane;
-        v[u] = c < nvec ? ld16(xr + c * VEC) : zero16();
+        v[u] = c < nvec ? ld16_stream(xr + c * VEC) : zero16();
       }
 #pragma unroll
       for (int u = 0; u < kCeBatch; ++u) {
         if (c0 + u * 64 + lane >= nvec) continue;
-        float y[VEC], vm = -__builtin_inff();
+        float xv[VEC], vm = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          y[i] = VecTraits<T>::get(v[u], i) * kLog2e;
-          vm = fmaxf(vm, y[i]);
+          xv[i] = VecTraits<T>::get(v[u], i);
+          vm = fmaxf(vm, xv[i]);
         }
-        const float mn = fmaxf(m, vm);
-        if (mn == -__builtin_inff()) continue;  // nothing above -inf yet
+        const float mn = fmaxf(m, vm * kLog2e);  // running max, base-2 units
+        if (mn == -__builtin_inff()) continue;   // nothing above -inf yet
         float vs = 0.f;
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) vs += exp2_fast(y[i] - mn);
+        for (int i = 0; i < VEC; ++i) vs += exp2_fast(__builtin_fmaf(xv[i], kLog2e, -mn));
         s = s * exp2_fast(m - mn) + vs;  // exp2(-inf) = 0 on the first vector
         m = mn;
       }
     }
   } else {
     for (int64_t j = lane; j < V; j += 64) {
-      const float y = to_f32<T>(xr[j]) * kLog2e;
-      const float mn = fmaxf(m, y);
+      const float xj = to_f32<T>(xr[j]);
+      const float mn = fmaxf(m, xj * kLog2e);
       if (mn == -__builtin_inff()) continue;
-      s = s * exp2_fast(m - mn) + exp2_fast(y - mn);
+      s = s * exp2_fast(m - mn) + exp2_fast(__builtin_fmaf(xj, kLog2e, -mn));
       m = mn;
     }
   }
@@ -110,7 +154,7 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ x, co
   const int64_t t = tgt[row];
   const bool on = t != ignore_index && t >= 0 && t < V;
   const float gs = on ? grad[0] * scale : 0.f;
-  const float l = lse[row];
+  const float l = lse[row], l2 = l * kLog2e;
   if (VECOK) {
     const int64_t nvec = V / VEC;
     for (int64_t c0 = 0; c0 < nvec; c0 += 64 * kCeBatch) {
@@ -118,25 +162,24 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ x, co
 #pragma unroll
       for (int u = 0; u < kCeBatch; ++u) {
         const int64_t c = c0 + u * 64 + lane;
-        v[u] = (on && c < nvec) ? ld16(xr + c * VEC) : zero16();
+        v[u] = (on && c < nvec) ? ld16_stream(xr + c * VEC) : zero16();
       }
 #pragma unroll
       for (int u = 0; u < kCeBatch; ++u) {
         const int64_t c = c0 + u * 64 + lane;
         if (c >= nvec) continue;
-        Vec16 o;
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-          const float p = on ? exp2_fast((VecTraits<T>::get(v[u], i) - l) * kLog2e) : 0.f;
-          const float hit = (c * VEC + i == t) ? 1.f : 0.f;
-          VecTraits<T>::set(o, i, gs * (p - hit));
+        Vec16 o = on ? CeVec<T>::grad(v[u], l2, gs) : zero16();
+        if (on && t / VEC == c) {  // the target's vector: g * (p - 1) there
+          const int i = (int)(t - c * VEC);
+          const float p = exp2_fast(__builtin_fmaf(VecTraits<T>::get(v[u], i), kLog2e, -l2));
+          VecTraits<T>::set(o, i, gs * (p - 1.f));
         }
-        st16(dr + c * VEC, o);
+        st16_stream(dr + c * VEC, o);
       }
     }
   } else {
     for (int64_t j = lane; j < V; j += 64) {
-      const float p = on ? exp2_fast((to_f32<T>(xr[j]) - l) * kLog2e) : 0.f;
+      const float p = on ? exp2_fast(__builtin_fmaf(to_f32<T>(xr[j]), kLog2e, -l2)) : 0.f;
       dr[j] = from_f32<T>(gs * (p - (j == t ? 1.f : 0.f)));
     }
   }
