@@ -22,6 +22,7 @@ namespace abacus {
 constexpr int kRouteTB = 16;   // tokens per router / permute block (one MFMA row tile)
 constexpr int kMaxE = 64;      // experts handled by the fused router
 constexpr int kMaxK = 8;       // slots per token handled by the fused kernels
+constexpr int64_t kScanLdsBytes = 48 * 1024;  // route_scan stages histograms up to this size in LDS
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -219,11 +220,23 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
 // experts) and base[b][e] = first dispatched row of block b's tokens for e.
 // Applies the auxiliary-loss-free bias step when requested.
 // ---------------------------------------------------------------------------
-template <typename T>
+// STAGED: the (nb, E) histogram is first copied into LDS by all threads in
+// 16-byte pieces (one round trip), and both passes read it there; otherwise
+// each thread walks its column in HBM twice.
+template <typename T, bool STAGED>
 __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restrict__ hist, int nb, int E,
                                                           int64_t R, T* __restrict__ bias, float speed,
                                                           int32_t* __restrict__ base, int32_t* __restrict__ counts,
                                                           int32_t* __restrict__ offsets) {
+  extern __shared__ int s_hist[];
+  if (STAGED) {
+    const int n = nb * E;
+    for (int i = threadIdx.x; i < n / 4; i += 1024)
+      reinterpret_cast<int4*>(s_hist)[i] = reinterpret_cast<const int4*>(hist)[i];
+    for (int i = n / 4 * 4 + (int)threadIdx.x; i < n; i += 1024) s_hist[i] = hist[i];
+    __syncthreads();
+  }
+  auto hv = [&](int b, int e) -> int { return STAGED ? s_hist[b * E + e] : hist[(int64_t)b * E + e]; };
   __shared__ int part[16][kMaxE];
   __shared__ int cnt[kMaxE];
   __shared__ int off[kMaxE + 1];
@@ -235,7 +248,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
   const int b1 = min(nb, b0 + per);
   int p = 0;
   if (e < E)
-    for (int b = b0; b < b1; ++b) p += hist[(int64_t)b * E + e];
+    for (int b = b0; b < b1; ++b) p += hv(b, e);
   part[q][e] = p;
   __syncthreads();
   if (tid < kMaxE) {
@@ -270,7 +283,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
     for (int i = 0; i < q; ++i) run += part[i][e];
     for (int b = b0; b < b1; ++b) {
       base[(int64_t)b * E + e] = run;
-      run += hist[(int64_t)b * E + e];
+      run += hv(b, e);
     }
   }
 }
@@ -451,7 +464,7 @@ __device__ inline void gating_bwd_token(int K, float rho, const float* dw, const
 }
 
 // ---------------------------------------------------------------------------
-// B1: combine backward + gating.  Per token: dy(t,k) = w(t,k) * dout[t]
+// B1: combine backward + gating.  Per token (a wave): dy(t,k) = w(t,k) * dout[t]
 // written to the dispatched row, dw(t,k) = <dout[t], y(t,k)>, then the
 // sigmoid / renormalise backward to dL/dlogit for the K selected experts.
 // ---------------------------------------------------------------------------
@@ -461,63 +474,68 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
                                                           const float* __restrict__ score,
                                                           const int32_t* __restrict__ pos, int T_, int D, int K,
                                                           float rho, T* __restrict__ dy, float* __restrict__ dlogit) {
+  // one token per wave: no barriers; each lane sums its part of the K dot
+  // products over its vectors in order, then one butterfly per slot
   constexpr int VEC = VecTraits<T>::kN;
-  __shared__ float s_red[4][kMaxK];
-  __shared__ int s_p[kMaxK];
-  __shared__ float s_w[kMaxK];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  constexpr int U = kGatherBatch;
+  const int lane = threadIdx.x & 63;
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= T_) return;
+  int p[kMaxK];
+  float w[kMaxK], dw[kMaxK];
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k) {
+    const bool on = k < K;
+    p[k] = on ? pos[(int64_t)t * K + k] : 0;
+    w[k] = on ? to_f32<T>(weights[(int64_t)t * K + k]) : 0.f;
+    dw[k] = 0.f;
+  }
   const int nvec = D / VEC;
-  for (int t = blockIdx.x; t < T_; t += gridDim.x) {
-    if (tid < K) {
-      s_p[tid] = pos[(int64_t)t * K + tid];
-      s_w[tid] = to_f32<T>(weights[(int64_t)t * K + tid]);
-    }
-    __syncthreads();
-    float dw[kMaxK];
+  for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
+    Vec16 g[U];
 #pragma unroll
-    for (int k = 0; k < kMaxK; ++k) dw[k] = 0.f;
-    for (int c = tid; c < nvec; c += 256) {
-      const Vec16 g = ld16(dout + (int64_t)t * D + c * VEC);
-#pragma unroll
-      for (int k = 0; k < kMaxK; ++k) {
-        if (k < K) {
-          const int64_t ro = (int64_t)s_p[k] * D + c * VEC;
-          const Vec16 v = ld16(y + ro);
-          Vec16 o;
-          float part = 0.f;
-#pragma unroll
-          for (int i = 0; i < VEC; ++i) {
-            const float gi = VecTraits<T>::get(g, i);
-            part += gi * VecTraits<T>::get(v, i);
-            VecTraits<T>::set(o, i, gi * s_w[k]);
-          }
-          dw[k] += part;
-          st16(dy + ro, o);
-        }
-      }
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * 64 + lane;
+      g[u] = c < nvec ? ld16(dout + (int64_t)t * D + c * VEC) : zero16();
     }
 #pragma unroll
     for (int k = 0; k < kMaxK; ++k) {
-      if (k < K) {
-        const float r = wave_sum(dw[k]);
-        if (lane == 0) s_red[wave][k] = r;
+      if (k >= K) break;
+      Vec16 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        v[u] = c < nvec ? ld16(y + (int64_t)p[k] * D + c * VEC) : zero16();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        if (c >= nvec) continue;
+        Vec16 o;
+        float part = 0.f;
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          const float gi = VecTraits<T>::get(g[u], i);
+          part += gi * VecTraits<T>::get(v[u], i);
+          VecTraits<T>::set(o, i, gi * w[k]);
+        }
+        dw[k] += part;
+        st16(dy + (int64_t)p[k] * D + c * VEC, o);
       }
     }
-    __syncthreads();
-    if (tid == 0) {
-      float dwt[kMaxK], w[kMaxK], s[kMaxK], dl[kMaxK];
-      float sum = 0.f;
-      for (int k = 0; k < K; ++k) {
-        dwt[k] = ((s_red[0][k] + s_red[1][k]) + s_red[2][k]) + s_red[3][k];
-        w[k] = s_w[k];
-        s[k] = score[(int64_t)t * K + k];
-        sum += s[k];
-      }
-      gating_bwd_token(K, rho, dwt, w, s, round_to<T>(sum), dl);
-      for (int k = 0; k < K; ++k) dlogit[(int64_t)t * K + k] = dl[k];
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxK; ++k)
+    if (k < K) dw[k] = wave_sum(dw[k]);
+  if (lane == 0) {
+    float sc[kMaxK], dl[kMaxK];
+    float sum = 0.f;
+    for (int k = 0; k < K; ++k) {
+      sc[k] = score[(int64_t)t * K + k];
+      sum += sc[k];
     }
-    __syncthreads();
+    gating_bwd_token(K, rho, dw, w, sc, round_to<T>(sum), dl);
+    for (int k = 0; k < K; ++k) dlogit[(int64_t)t * K + k] = dl[k];
   }
 }
 
@@ -983,12 +1001,19 @@ int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, 
   ABACUS_CHECK_ARG(T >= 0 && T * K < (1ll << 31), "bad token count %lld", (long long)T);
   hipStream_t s = (hipStream_t)stream;
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(route_scan_kernel<uint16_t>, dim3(1), dim3(1024), 0, s, hist, nb, (int)E, T * K,
-                       (uint16_t*)bias_E, bias_update_speed, base, counts_E, offsets_E1);
-  else
-    hipLaunchKernelGGL(route_scan_kernel<float>, dim3(1), dim3(1024), 0, s, hist, nb, (int)E, T * K,
-                       (float*)bias_E, bias_update_speed, base, counts_E, offsets_E1);
+  const int64_t hist_bytes = (int64_t)nb * E * 4;
+  const bool staged = hist_bytes <= kScanLdsBytes && (uintptr_t)hist % 16 == 0;
+#define ABACUS_SCAN(TT, ST)                                                                                 \
+  hipLaunchKernelGGL((route_scan_kernel<TT, ST>), dim3(1), dim3(1024), ST ? (unsigned)hist_bytes : 0u, s, hist, \
+                     nb, (int)E, T * K, (TT*)bias_E, bias_update_speed, base, counts_E, offsets_E1)
+  if (dtype == kBF16) {
+    if (staged) ABACUS_SCAN(uint16_t, true);
+    else ABACUS_SCAN(uint16_t, false);
+  } else {
+    if (staged) ABACUS_SCAN(float, true);
+    else ABACUS_SCAN(float, false);
+  }
+#undef ABACUS_SCAN
   ABACUS_CHECK_LAUNCH("route_scan");
   return 0;
 }
@@ -1033,7 +1058,8 @@ int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* we
   if (check_route_shape(T, D, K, K, dtype)) return 1;
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
-  const int grid = (int)std::min<int64_t>(T, 1 << 20);
+  ABACUS_CHECK_ARG(T <= (int64_t)INT_MAX - 3, "too many tokens (%lld)", (long long)T);
+  const unsigned grid = (unsigned)((T + 3) / 4);  // a token per wave
   if (dtype == kBF16)
     hipLaunchKernelGGL(combine_bwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)dout_TD,
                        (const uint16_t*)y_RD, (const uint16_t*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
