@@ -929,7 +929,7 @@ int check_dtype(int dtype) {
 int check_route_shape(int64_t T, int64_t D, int64_t E, int64_t K, int dtype, bool need_vec = true) {
   if (check_dtype(dtype)) return 1;
   ABACUS_CHECK_ARG(T >= 0 && T < (1ll << 31), "token count %lld out of range", (long long)T);
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
   ABACUS_CHECK_ARG(K >= 1 && K <= E && K <= kMaxK, "top_k %lld: must be in [1, min(n_experts, %d)]",
                    (long long)K, kMaxK);
   ABACUS_CHECK_ARG(D >= 1 && D < (1ll << 31), "dim %lld out of range", (long long)D);
@@ -997,7 +997,7 @@ int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, 
                           float bias_update_speed, int dtype, int32_t* base, int32_t* counts_E,
                           int32_t* offsets_E1, void* stream) {
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
   ABACUS_CHECK_ARG(T >= 0 && T * K < (1ll << 31), "bad token count %lld", (long long)T);
   hipStream_t s = (hipStream_t)stream;
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
@@ -1075,7 +1075,7 @@ int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* we
 int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const float* score_TK, int64_t T,
                              int64_t K, float route_scale, int dtype, float* dlogit_TK, void* stream) {
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(K >= 1 && K <= kMaxK, "top_k %lld: this build supports 1..%d", (long long)K, kMaxK);
+  ABACUS_CHECK_ARG(K >= 1 && K <= kMaxK, "top_k %lld: supported range 1..%d", (long long)K, kMaxK);
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   const int grid = (int)((T + 255) / 256);
@@ -1160,7 +1160,7 @@ int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E) {
 int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
                             int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream) {
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
   ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
   hipStream_t s = (hipStream_t)stream;
   const bool reg = router_wgrad_reg_path(D, E, dtype);
@@ -1215,7 +1215,7 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
 int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, float speed, int dtype, void* bias_E,
                               void* stream) {
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: this build supports 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == kBF16)
     hipLaunchKernelGGL(update_bias_kernel<uint16_t>, dim3(1), dim3(1024), 0, s, indices, N, (int)E, speed,

@@ -41,7 +41,7 @@ class AdamW:
             raise ValueError(f"Invalid weight decay: {weight_decay}")
         if owned is not None or grad_shards is not None:
             raise NotImplementedError("ZeRO-sharded optimizer state needs several data-parallel ranks; "
-                                      "this build runs on one GPU")
+                                      "abacus_amd runs on one GPU")
         self.params = list(model.parameters())
         self.lr = lr
         self.beta1 = betas[0]

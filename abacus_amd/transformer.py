@@ -13,14 +13,17 @@ reference's:
   TransformerBlockMoe  abacus/transformer_block.py:64-110
   TransformerMoe       abacus/transformer_moe.py:17-75
 
-The MoE layer inside each block is abacus_amd.moe.MoE (the HIP path).  The
-rest runs on torch.  Causal attention on the GPU is torch's fused kernel
-(flash / memory-efficient: the (L, L) scores never reach HBM, and stay fp32
-where the reference rounds them to the activation dtype); on the CPU, or for
-inputs no fused kernel takes, it is materialised like the reference's (scores,
-mask, softmax, weighted sum) as one autograd function whose batched products
-all take contiguous operands.  Tensor, sequence and context parallelism with
-more than one process are not part of this build.
+The MoE layer inside each block is abacus_amd.moe.MoE (the HIP path).  On
+the GPU, RMSNorm, the q/k norms fused with the rotary embedding, and causal
+attention in bf16 with head dim 64 (L a multiple of 128) also run on this
+library's HIP kernels; the (L, L) scores never reach HBM and stay fp32 where
+the reference rounds them to the activation dtype.  Other attention inputs go
+to torch's fused causal kernels (flash / memory-efficient), and on the CPU,
+or for inputs no fused kernel takes, attention is materialised like the
+reference's (scores, mask, softmax, weighted sum) as one autograd function
+whose batched products all take contiguous operands.  The dense projections
+and the embedding run on torch.  Tensor, sequence and context parallelism
+with more than one process are not implemented here (one GPU).
 """
 
 from __future__ import annotations
@@ -258,7 +261,7 @@ class _CausalAttention(torch.autograd.Function):
 # Fused causal attention on the GPU: torch's flash / memory-efficient
 # kernels (scores and probabilities stay on chip, in fp32), never its
 # materializing math path.  Inputs neither kernel takes fall back to
-# _CausalAttention; the verdict is kept per (dtype, head_dim).
+# _CausalAttention; the outcome is kept per (dtype, head_dim).
 _FUSED_BACKENDS = None
 _fused_ok: dict = {}
 

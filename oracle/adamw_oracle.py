@@ -1,6 +1,6 @@
 """Oracle: CPU restatement of abacus's AdamW step. TEST INFRASTRUCTURE ONLY.
 
-Only tests/ may use this module, and only as the checker -- never as part of
+Only tests/ may use this module, and only to check results -- never as part of
 the product path.
 
 It restates abacus/optimizers/adamw.py:85-119 (AdamW.step) element by element

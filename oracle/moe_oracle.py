@@ -1,7 +1,7 @@
 """Oracle: CPU restatement of abacus's MoE layer. TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
-this module, and only as the checker (or the timed CPU baseline) -- never as
+this module, and only to check results (or as the timed CPU baseline) -- never as
 part of the product path.
 
 It restates, in this project's own code, the algorithm of
