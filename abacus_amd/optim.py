@@ -17,7 +17,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["AdamW"]
+__all__ = ["AdamW", "WSD"]
 
 
 class AdamW:
@@ -85,3 +85,33 @@ class AdamW:
             steps = (ctypes.c_int64 * n)(*[it[4] for it in items])
             _lib.call("abacus_adamw_step", *ptrs, numels, steps, n, self.lr, self.beta1, self.beta2, self.eps,
                       self.weight_decay, _lib.dtype_code(dtype), _lib.stream_of(device))
+
+
+class WSD:
+    """Warmup-stable-decay learning rate (optimizers/lr_scheduler.py): linear warmup over the
+    first 2% of steps, constant, then linear decay to 0 over the last 10%."""
+
+    def __init__(self, total_steps: int, lr: float = 5e-4):
+        if total_steps < 1:
+            raise ValueError(f"total_steps must be at least 1, got {total_steps}")
+        if lr < 0:
+            raise ValueError(f"Invalid learning rate: {lr}")
+        self.total_steps = total_steps
+        self.lr = lr
+        self.warmup_steps = total_steps * 2 // 100
+        self.decay_steps = total_steps * 10 // 100
+        self._step = 0
+
+    def learning_rate(self, step: int) -> float:
+        if step < 1 or step > self.total_steps:
+            raise ValueError(f"step must be in 1..{self.total_steps}, got {step}")
+        if self.warmup_steps > 0 and step <= self.warmup_steps:
+            return self.lr * step / self.warmup_steps
+        if self.decay_steps > 0 and step > self.total_steps - self.decay_steps:
+            done = (step - (self.total_steps - self.decay_steps)) / self.decay_steps
+            return self.lr * (1 - done)
+        return self.lr
+
+    def step(self) -> float:
+        self._step += 1
+        return self.learning_rate(self._step)

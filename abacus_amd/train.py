@@ -5,6 +5,10 @@ backward, one AdamW step.  The optimizer is abacus_amd.optim.AdamW, the
 reference AdamW (optimizers/adamw.py) with its defaults (lr 1e-3, betas
 (0.9, 0.999), eps 1e-8, weight decay 1e-2, decoupled) and its per-op
 rounding, as one HIP pass per group of tensors.
+
+``Trainer`` and ``get_device`` mirror trainer.py's single-process API, and
+``cross_entropy`` / ``set_use_liger`` mirror kernels/liger.py; on the GPU the
+cross-entropy is this library's HIP kernel pair either way.
 """
 
 from __future__ import annotations
@@ -12,10 +16,13 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from . import _lib
-from .optim import AdamW
+import os
 
-__all__ = ["make_optimizer", "next_token_loss", "train_step"]
+from . import _lib
+from .optim import WSD, AdamW
+
+__all__ = ["Trainer", "cross_entropy", "get_device", "make_optimizer", "next_token_loss", "set_use_liger",
+           "train_step"]
 
 
 class _CrossEntropyFunction(torch.autograd.Function):
@@ -29,7 +36,8 @@ class _CrossEntropyFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, logits_NV, targets_N, count: int, ignore_index: int):
+    def forward(ctx, logits_NV, targets_N, count, ignore_index: int):
+        # count: the rows not ignored, a Python int or a device scalar tensor
         N, V = logits_NV.shape
         dev = logits_NV.device
         lse = torch.empty(N, dtype=torch.float32, device=dev)
@@ -44,12 +52,50 @@ class _CrossEntropyFunction(torch.autograd.Function):
     def backward(ctx, g):
         logits_NV, targets_N, lse = ctx.saved_tensors
         N, V = logits_NV.shape
-        g = g.float().contiguous()
+        if torch.is_tensor(ctx.count):  # fold 1 / count into g on the device
+            g, scale = (g.float() / ctx.count).contiguous(), 1.0
+        else:
+            g, scale = g.float().contiguous(), 1.0 / ctx.count
         d_logits = torch.empty_like(logits_NV)
         _lib.call("abacus_cross_entropy_bwd", _lib.ptr(logits_NV), _lib.ptr(targets_N), _lib.ptr(lse), _lib.ptr(g),
-                  1.0 / ctx.count, N, V, ctx.ignore_index, _lib.dtype_code(logits_NV.dtype), _lib.ptr(d_logits),
+                  scale, N, V, ctx.ignore_index, _lib.dtype_code(logits_NV.dtype), _lib.ptr(d_logits),
                   _lib.stream_of(logits_NV.device))
         return d_logits, None, None, None
+
+
+_use_liger = False
+
+
+def set_use_liger(enabled: bool) -> None:
+    """kernels/liger.py:7-9.  On the GPU both settings run the HIP kernels; with it set, CPU
+    inputs raise, as the reference's liger path does."""
+    global _use_liger
+    _use_liger = enabled
+
+
+def cross_entropy(input: torch.Tensor, target: torch.Tensor, weight: torch.Tensor | None = None,
+                  size_average: bool | None = None, ignore_index: int = -100, reduce: bool | None = None,
+                  reduction: str = "mean", label_smoothing: float = 0.0) -> torch.Tensor:
+    """kernels/liger.py:12-47: torch.nn.functional.cross_entropy's signature and result.
+
+    (N, V) GPU logits in fp32 or bf16 with the default options (mean over the rows whose
+    target is not ignore_index, no class weights or label smoothing) take the HIP kernels,
+    with no host sync: the row count stays on the device.  Everything else is torch's
+    cross_entropy.  A target outside [0, V) other than ignore_index contributes no loss
+    there (torch's GPU kernel stops on a device assertion instead).
+    """
+    if _use_liger and input.device.type != "cuda":
+        raise RuntimeError("Liger cross entropy needs a CUDA tensor")
+    fused = (input.is_cuda and input.dim() == 2 and input.dtype in (torch.float32, torch.bfloat16)
+             and target.dim() == 1 and target.shape[0] == input.shape[0] and weight is None
+             and size_average is None and reduce is None and reduction == "mean" and label_smoothing == 0.0)
+    if not fused:
+        return F.cross_entropy(input, target, weight=weight, size_average=size_average, ignore_index=ignore_index,
+                               reduce=reduce, reduction=reduction, label_smoothing=label_smoothing)
+    t = target.to(torch.int64).contiguous()
+    V = input.shape[1]
+    count = ((t != ignore_index) & (t >= 0) & (t < V)).sum().to(torch.float32)
+    return _CrossEntropyFunction.apply(input.contiguous(), t, count, int(ignore_index)).to(input.dtype)
 
 
 def make_optimizer(model: torch.nn.Module, lr: float = 1e-3) -> AdamW:
@@ -93,3 +139,51 @@ def train_step(model: torch.nn.Module, optimizer: AdamW, tokens_BL: torch.Tensor
     loss.backward()
     optimizer.step()
     return loss.detach()
+
+
+def get_device() -> torch.device:
+    """trainer.py:21-26: the GPU of LOCAL_RANK (made current), or the CPU without one."""
+    if not torch.cuda.is_available():
+        return torch.device("cpu")
+    local_rank = int(os.environ.get("LOCAL_RANK", "0"))
+    torch.cuda.set_device(local_rank)
+    return torch.device("cuda", local_rank)
+
+
+class Trainer:
+    """trainer.py:29-103, the single-process path: the model moved to the device, the
+    reference's AdamW with its defaults, and the WSD schedule when total_steps is given.
+    Data, pipeline and context parallelism need several processes and are refused."""
+
+    def __init__(self, model: torch.nn.Module, parallel=None, pipeline=None, total_steps: int | None = None):
+        if parallel is not None and pipeline is not None:
+            raise ValueError("pipeline parallel does not use DataParallel")
+        if parallel is not None or pipeline is not None:
+            raise NotImplementedError("data and pipeline parallelism need several processes; abacus_amd runs on "
+                                      "one GPU")
+        self.device = get_device()
+        self.model = model.to(self.device)
+        self.parallel = None
+        self.pipeline = None
+        self.optimizer = AdamW(self.model)
+        self.scheduler = WSD(total_steps) if total_steps is not None else None
+        if self.scheduler is not None:
+            self.optimizer.lr = self.scheduler.learning_rate(1)
+
+    def step(self, tokens_BL: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(loss, local loss), both the step's mean next-token cross-entropy on one process."""
+        self.model.train()
+        tokens_BL = tokens_BL.to(self.device)
+        inputs_BL = tokens_BL.clamp(min=0)  # -100 is padding; the embedding has no row for it
+        logits = self.model(inputs_BL)  # (B, L, vocab)
+        loss = next_token_loss(logits, tokens_BL)
+        self.optimizer.zero_grad()
+        loss.backward()
+        local_loss = loss.detach()
+        self._optimizer_step()
+        return loss.detach(), local_loss
+
+    def _optimizer_step(self) -> None:
+        if self.scheduler is not None:
+            self.optimizer.lr = self.scheduler.step()
+        self.optimizer.step()

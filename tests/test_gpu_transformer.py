@@ -205,3 +205,48 @@ def test_rmsnorm_rope_matches_fp64(dtype, shape):
     rtol = RTOL[dtype]
     for name, a, r, t in zip(("y", "dx", "dgamma"), got, ref, tru):
         assert _rel(a, t) <= max(2 * _rel(r, t), rtol), f"{name}: gpu {_rel(a, t):.3g} vs cpu {_rel(r, t):.3g}"
+
+
+def test_trainer_step_matches_train_step():
+    """abacus.trainer.Trainer(model).step (trainer.py:58-97, one process) is train_step with the
+    reference's AdamW defaults: the same losses, parameters and moments over two steps; with
+    total_steps the WSD rate is applied before each step."""
+    from abacus.trainer import Trainer
+    torch.manual_seed(23)
+    model = TransformerMoe(vocab_size=512, dim=128, n_heads=2, head_dim=64, n_blocks=2, n_experts=4, top_k=2,
+                           hidden_dim=256).to(torch.bfloat16).cuda()
+    twin = copy.deepcopy(model)
+    trainer = Trainer(model)
+    opt = make_optimizer(twin)
+    gen = torch.Generator().manual_seed(6)
+    for _ in range(2):
+        tokens = torch.randint(0, 512, (2, 128), generator=gen)
+        tokens[0, 5] = -100
+        loss, local = trainer.step(tokens)
+        want = train_step(twin, opt, tokens.cuda())
+        assert torch.equal(loss, want) and torch.equal(local, want)
+    for (name, pa), pb in zip(model.named_parameters(), twin.parameters()):
+        assert torch.equal(pa, pb), name
+    scheduled = Trainer(copy.deepcopy(twin), total_steps=100)
+    assert scheduled.optimizer.lr == scheduled.scheduler.learning_rate(1)
+    scheduled.step(torch.randint(0, 512, (2, 128), generator=gen))
+    assert scheduled.optimizer.lr == scheduled.scheduler.learning_rate(1)  # step 1 of 100: warmup 1/2
+
+
+def test_liger_cross_entropy_matches_torch_on_gpu():
+    """abacus.kernels.liger.cross_entropy on GPU logits: the HIP kernels with the row count kept
+    on the device, against fp64; all rows ignored gives NaN, as torch's mean does."""
+    from abacus.kernels.liger import cross_entropy
+    g = torch.Generator(device="cuda").manual_seed(8)
+    x = (torch.randn(500, 32000, device="cuda", generator=g) * 2).to(torch.bfloat16).requires_grad_()
+    t = torch.randint(0, 32000, (500,), device="cuda", generator=g)
+    t[::5] = -100
+    loss = cross_entropy(x, t)
+    (grad,) = torch.autograd.grad(loss, x)
+    ref_x = x.detach().double().requires_grad_()
+    ref = F.cross_entropy(ref_x, t)
+    (ref_grad,) = torch.autograd.grad(ref, ref_x)
+    assert loss.dtype == torch.bfloat16
+    assert abs(float(loss.detach()) - float(ref.detach())) <= 2 ** -8 * abs(float(ref.detach()))
+    assert float((grad.double() - ref_grad).norm() / ref_grad.norm()) < 4e-3
+    assert torch.isnan(cross_entropy(x.detach(), torch.full_like(t, -100)))
