@@ -17,7 +17,7 @@
 //   O^T = V^T P^T: lane l accumulates output dims 8g + 4h + 0..3 of the same
 //   query, so rescaling a row is one factor per lane.  P^T's operand (8
 //   consecutive keys of the lane's query) is built from the score registers
-//   with one 64-bit exchange between lanes l and l ^ 32.
+//   with two v_permlane32_swap between lanes l and l ^ 32.
 #include <type_traits>
 
 #include "common.h"
@@ -79,25 +79,46 @@ __device__ inline Vec16 frag_vt(const char* tile, int d0, int c, int lane) {
   return v;
 }
 
+// v_permlane32_swap: lanes 32..63 of a take lanes 0..31 of b, and lanes 0..31
+// of b take lanes 32..63 of a (one VALU instruction, no LDS round trip).
+__device__ inline void swap_halves(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+
+// max and sum of a value over lanes l and l ^ 32 (the same on both lanes)
+__device__ inline float pair_max(float x) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  swap_halves(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ inline float pair_sum(float x) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  swap_halves(a, b);  // lanes < 32: (own, partner); lanes >= 32: (partner, own)
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
 // MFMA operand of 8 consecutive rows from the score layout.  s holds a 32-row
-// half of a lane's column: rows 8g + 4h + 0..3 (g = 0..3) in registers 4g ..
-// 4g+3.  The operand for 16-row chunk c2 of the half needs rows 8h .. 8h + 7
-// of the chunk: lane h = 0 holds 0..3 and 8..11 of it, lane h = 1 holds 4..7
-// and 12..15, so each sends the pair the other needs (one 64-bit exchange
-// between lanes l and l ^ 32).  Values are rounded to bf16 on the way.
-__device__ inline Vec16 row_chunk_operand(const attn_f32x16& s, int c2, int h) {
+// half of a lane's column: rows 8g + 4h + 0..3 (g = 0..3, h = l / 32) in
+// registers 4g .. 4g+3.  The operand for 16-row chunk c2 of the half needs
+// rows 8h .. 8h + 7 of the chunk: lane h = 0 holds 0..3 (a) and 8..11 (b) of
+// it, lane h = 1 holds 4..7 (a) and 12..15 (b).  Swapping a of the upper
+// half with b of the lower half leaves lanes h = 0 with (a, b) = rows 0..7
+// and lanes h = 1 with rows 8..15.  Values are rounded to bf16 on the way.
+__device__ inline Vec16 row_chunk_operand(const attn_f32x16& s, int c2) {
   const int r0 = 8 * c2;
-  const uint32_t a0 = pack_bf16x2(s[r0 + 0], s[r0 + 1]);
-  const uint32_t a1 = pack_bf16x2(s[r0 + 2], s[r0 + 3]);
-  const uint32_t b0 = pack_bf16x2(s[r0 + 4], s[r0 + 5]);
-  const uint32_t b1 = pack_bf16x2(s[r0 + 6], s[r0 + 7]);
-  const uint32_t x0 = (uint32_t)__shfl_xor((int)(h ? a0 : b0), 32, 64);
-  const uint32_t x1 = (uint32_t)__shfl_xor((int)(h ? a1 : b1), 32, 64);
+  uint32_t a0 = pack_bf16x2(s[r0 + 0], s[r0 + 1]);
+  uint32_t a1 = pack_bf16x2(s[r0 + 2], s[r0 + 3]);
+  uint32_t b0 = pack_bf16x2(s[r0 + 4], s[r0 + 5]);
+  uint32_t b1 = pack_bf16x2(s[r0 + 6], s[r0 + 7]);
+  swap_halves(a0, b0);
+  swap_halves(a1, b1);
   Vec16 pf;
-  pf.w[0] = h ? x0 : a0;
-  pf.w[1] = h ? x1 : a1;
-  pf.w[2] = h ? b0 : x0;
-  pf.w[3] = h ? b1 : x1;
+  pf.w[0] = a0;
+  pf.w[1] = a1;
+  pf.w[2] = b0;
+  pf.w[3] = b1;
   return pf;
 }
 
@@ -193,7 +214,7 @@ __device__ __attribute__((always_inline)) inline void attn_fwd_block(const uint1
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kh][r]);
     // (-inf for a row whose keys in this tile all follow it; the running max is
     // finite from tile 0 on, as key 0 precedes every query)
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+    mx = pair_max(mx) * scale_log2;
     // Lazy rescale: the running max moves only when a row's max grows by
     // more than 8 (base 2), so probabilities stay below 2^8 and most tiles
     // skip rescaling the output accumulators (the wave decides together).
@@ -217,12 +238,11 @@ __device__ __attribute__((always_inline)) inline void attn_fwd_block(const uint1
         s[kh][r] = p;
         rs += p;
       }
-    rs += __shfl_xor(rs, 32, 64);
-    l_run += rs;
+    l_run += pair_sum(rs);
     // O^T += V^T P^T over the four 16-key chunks
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const Vec16 pf = row_chunk_operand(s[c >> 1], c & 1, h);
+      const Vec16 pf = row_chunk_operand(s[c >> 1], c & 1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) mfma32(oacc[t], frag_vt(vt, 32 * t, c, lane), pf);
     }
@@ -368,7 +388,7 @@ __device__ __attribute__((always_inline)) inline void attn_bwd_dq_block(
       }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const Vec16 zf = row_chunk_operand(sc[c >> 1], c & 1, h);
+      const Vec16 zf = row_chunk_operand(sc[c >> 1], c & 1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) mfma32(dqacc[t], frag_vt(kt, 32 * t, c, lane), zf);
     }
@@ -502,8 +522,8 @@ __device__ __attribute__((always_inline)) inline void attn_bwd_dkdv_block(
 #pragma unroll
       for (int c2 = 0; c2 < 2; ++c2) {
         const int c = 2 * qh + c2;  // 16-query chunk of the tile
-        const Vec16 pf = row_chunk_operand(pz, c2, h);
-        const Vec16 zf = row_chunk_operand(sc, c2, h);
+        const Vec16 pf = row_chunk_operand(pz, c2);
+        const Vec16 zf = row_chunk_operand(sc, c2);
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           mfma32(dvacc[t], frag_vt(dt, 32 * t, c, lane), pf);
