@@ -513,18 +513,26 @@ constexpr int LOADS_PER_TILE = 2 * DMA_PER_OPERAND; // DMA instructions per thre
 // Row-grouped kinds cut each expert's rows into BM-row tiles; a remainder of
 // at most THIN rows goes to a thin tile of THIN rows (same 256 columns, same
 // MFMAs and k order, so the same results) instead of a mostly empty full one.
+// Thin tiles run a 3-stage ring (3 x 48 KB): with few rows per expert they
+// mostly stream weights, and a third stage doubles the DMA a CU keeps in
+// flight (gate/up forward at 6 rows per expert 205 -> 184 us; Mixtral's
+// remainder tiles 1889 -> 1847 us).  Full tiles keep 2 stages (2 x 64 KB).
 constexpr int THIN = 128;
+constexpr int THIN_STAGES = 3;
 template <int BMT>
 struct Geo {
   static_assert(BMT == BM || BMT == THIN, "full or thin tiles");
   static constexpr int WTM = BMT / WAVES_M, FM = WTM / 32;
   static constexpr int A_BYTES = BMT * BK * 2;                 // A operand tile
   static constexpr int STAGE = A_BYTES + TILE_BYTES;           // A + B
+  static constexpr int ST = BMT == BM ? STAGES : THIN_STAGES;  // ring depth
   static constexpr int DMA_A = A_BYTES / 16 / NT, DMA_B = DMA_PER_OPERAND;
   static constexpr int LOADS = DMA_A + DMA_B;                  // DMA instructions per thread per k-tile
-  static constexpr int LDS = STAGES * STAGE > BMT * LDC * 2 ? STAGES * STAGE : BMT * LDC * 2;
+  static constexpr int LDS = ST * STAGE > BMT * LDC * 2 ? ST * STAGE : BMT * LDC * 2;
 };
-static_assert(Geo<BM>::LDS == LDS_BYTES && Geo<THIN>::LDS <= LDS_BYTES, "full tiles size the LDS");
+static_assert(Geo<BM>::LDS == LDS_BYTES, "full tiles");
+constexpr int LDS_ALLOC = Geo<THIN>::LDS > LDS_BYTES ? Geo<THIN>::LDS : LDS_BYTES;
+static_assert(LDS_ALLOC <= 160 * 1024, "LDS is 160 KB per work-group");
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -750,7 +758,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   using GE = Geo<BMT>;
   static_assert(!KT::WGRAD || BMT == BM, "weight gradients have full tiles only");
   constexpr int FM = GE::FM, WTM = GE::WTM, STAGE_BYTES = GE::STAGE, A_BYTES = GE::A_BYTES;
-  constexpr int LOADS_PER_TILE = GE::LOADS, DMA_A = GE::DMA_A;
+  constexpr int LOADS_PER_TILE = GE::LOADS, DMA_A = GE::DMA_A, ST = GE::ST;
   static_assert(!KindTraits<KIND>::DUAL_B || FN % 2 == 0, "dual-B pairs gate/up fragments");
   constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
 
@@ -823,7 +831,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   char* dma_stage = lds;
   int dma_k0 = 0;
   auto prep = [&](int kt) __attribute__((always_inline)) {
-    dma_stage = lds + (kt % STAGES) * STAGE_BYTES;
+    dma_stage = lds + (kt % ST) * STAGE_BYTES;
     kt += kbase;  // the k-tile within the whole reduction
     const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
     if (KT::DUAL_K && half != half_set) {  // second half of the concatenated k range
@@ -899,9 +907,9 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 
   // Wait until tile kt+1 has landed: `later` tiles were issued after it.
   auto wait_next = [&](int later) __attribute__((always_inline)) {
-    if (STAGES >= 5 && later >= 3) wait_vmcnt<(STAGES >= 5 ? 3 : 0) * LOADS_PER_TILE>();
-    else if (STAGES >= 4 && later >= 2) wait_vmcnt<(STAGES >= 4 ? 2 : 0) * LOADS_PER_TILE>();
-    else if (STAGES >= 3 && later >= 1) wait_vmcnt<(STAGES >= 3 ? 1 : 0) * LOADS_PER_TILE>();
+    if (ST >= 5 && later >= 3) wait_vmcnt<(ST >= 5 ? 3 : 0) * LOADS_PER_TILE>();
+    else if (ST >= 4 && later >= 2) wait_vmcnt<(ST >= 4 ? 2 : 0) * LOADS_PER_TILE>();
+    else if (ST >= 3 && later >= 1) wait_vmcnt<(ST >= 3 ? 1 : 0) * LOADS_PER_TILE>();
     else wait_vmcnt<0>();
   };
 
@@ -909,38 +917,38 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // stage.  Before the last step, one barrier: every wave has its reads of
   // this stage back (so the stage can be refilled) and has seen its DMA of
   // tile kt+1 land (so that tile can be read).  The last step's MFMAs then
-  // cover the first reads of tile kt+1 and the DMA of tile kt+STAGES into
+  // cover the first reads of tile kt+1 and the DMA of tile kt+ST into
   // this stage.
   auto ktile = [&](int kt, bool next, bool dma_next) __attribute__((always_inline)) {
-    char* st = lds + (kt % STAGES) * STAGE_BYTES;
-    char* st_next = lds + ((kt + 1) % STAGES) * STAGE_BYTES;
+    char* st = lds + (kt % ST) * STAGE_BYTES;
+    char* st_next = lds + ((kt + 1) % ST) * STAGE_BYTES;
 #pragma unroll
     for (int t = 0; t < NSTEP - 1; ++t) kstep(t & 1, true, st, t + 1, (t + 1) & 1, false);
-    // tiles kt+2 .. min(kt+STAGES-1, ktiles-1) may still be in flight
-    wait_next(min(STAGES - 2, ktiles - 2 - kt));
+    // tiles kt+2 .. min(kt+ST-1, ktiles-1) may still be in flight
+    wait_next(min(ST - 2, ktiles - 2 - kt));
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of the stage are back
     __syncthreads();
-    if (dma_next) prep(kt + STAGES);
+    if (dma_next) prep(kt + ST);
     __builtin_amdgcn_sched_barrier(0);
     kstep((NSTEP - 1) & 1, next, st_next, 0, 0, dma_next);
   };
 
-  // prologue: tiles 0 .. STAGES-1 in flight, tile 0's first fragments read.
+  // prologue: tiles 0 .. ST-1 in flight, tile 0's first fragments read.
   // A tile with no k range (an empty wgrad segment) keeps zero accumulators.
   if (ktiles > 0) {
 #pragma unroll
-    for (int p = 0; p < STAGES; ++p)
+    for (int p = 0; p < ST; ++p)
       if (p < ktiles) {
         prep(p);
 #pragma unroll
         for (int n = 0; n < LOADS_PER_TILE; ++n) dma(n);
       }
-    // tile 0 landed: tiles 1 .. min(STAGES, ktiles) - 1 may be in flight
+    // tile 0 landed: tiles 1 .. min(ST, ktiles) - 1 may be in flight
     {
-      const int later = min(STAGES, ktiles) - 1;
-      if (STAGES >= 5 && later >= 4) wait_vmcnt<(STAGES >= 5 ? 4 : 0) * LOADS_PER_TILE>();
-      else if (STAGES >= 4 && later >= 3) wait_vmcnt<(STAGES >= 4 ? 3 : 0) * LOADS_PER_TILE>();
-      else if (STAGES >= 3 && later >= 2) wait_vmcnt<(STAGES >= 3 ? 2 : 0) * LOADS_PER_TILE>();
+      const int later = min(ST, ktiles) - 1;
+      if (ST >= 5 && later >= 4) wait_vmcnt<(ST >= 5 ? 4 : 0) * LOADS_PER_TILE>();
+      else if (ST >= 4 && later >= 3) wait_vmcnt<(ST >= 4 ? 3 : 0) * LOADS_PER_TILE>();
+      else if (ST >= 3 && later >= 2) wait_vmcnt<(ST >= 3 ? 2 : 0) * LOADS_PER_TILE>();
       else if (later >= 1) wait_vmcnt<LOADS_PER_TILE>();
       else wait_vmcnt<0>();
     }
@@ -950,7 +958,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 
     // steady state, then the last tiles (no DMA; no next tile for the last)
     int kt = 0;
-    for (; kt + STAGES < ktiles; ++kt) ktile(kt, true, true);
+    for (; kt + ST < ktiles; ++kt) ktile(kt, true, true);
     for (; kt + 1 < ktiles; ++kt) ktile(kt, true, false);
     ktile(kt, false, false);
   }
@@ -1093,7 +1101,9 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 // counters; the last of a launch's P blocks to finish sets its slot back to
 // zero for the next launch that uses it.
 constexpr int kCtrSlots = 64;
-constexpr int kMaxExperts = 4096;  // the expert offsets a block keeps in LDS (check_gemm_shape's bound)
+// The expert offsets a block keeps in LDS (check_gemm_shape's bound); with
+// the thin tiles' 144 KB ring the pair launches then stay within 160 KB.
+constexpr int kMaxExperts = 1024;
 __device__ int g_tile_ctr[kCtrSlots][16] = {};  // [0..7] next tile of each XCD's share, [8] blocks done
 
 __device__ inline int xcc_id() { return __builtin_amdgcn_s_getreg((31 << 11) | 20) & 7; }  // HW_REG_XCC_ID
@@ -1341,7 +1351,7 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
 
 template <int KIND>
 __global__ __launch_bounds__(NT, 1) void gemm_bf16_wgrad_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_ALLOC];
   __shared__ int next_s;
   __shared__ int offs_s[kMaxExperts + 1];
   gemm_wgrad_tiles<KIND>(g, (int)gridDim.x, lds, &next_s, offs_s);
@@ -1356,7 +1366,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_wgrad_kernel(GemmArgs g) {
 template <int KR, int KW>
 __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, GemmArgs g2, GemmArgs g3, int n1,
                                                                int n2) {
-  __shared__ __attribute__((aligned(1024))) char lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_ALLOC];
   const int b = blockIdx.x;
   if (b < n1) {
     gemm_tile<KR, BM>(g1, b, n1, lds);
