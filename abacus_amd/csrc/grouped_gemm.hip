@@ -1804,10 +1804,16 @@ int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t*
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   if (R == 0) return 0;
   const GemmArgs g = args_down_fwd(h_RM, w_down_EMD, offsets_E1, R, M, D, E, y_RD);
-  if (pipe_ok<kDownFwd>(dtype, g) && ws != nullptr) {
-    const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);
-    if (plan.on() && ws_bytes >= plan.ws_bytes())
-      return launch_pipe_split<kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd");
+  if (pipe_ok<kDownFwd>(dtype, g)) {
+    // At most THIN rows per expert on average (small batches): thin tiles,
+    // which stream the weights without DMA of padding rows.
+    if (R <= (int64_t)pipe::THIN * E)
+      return launch_rows<kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd");
+    if (ws != nullptr) {
+      const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);
+      if (plan.on() && ws_bytes >= plan.ws_bytes())
+        return launch_pipe_split<kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd");
+    }
   }
   return dispatch_gemm<kDownFwd>(dtype, g, (int)R, (hipStream_t)stream, "down_fwd");
 }

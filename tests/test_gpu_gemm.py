@@ -162,11 +162,15 @@ def test_down_fwd_split_tail():
         assert err < 1e-2, f"expert {e}: relative error {err:.3g}"
 
 
-def test_row_tiles_every_remainder_class():
+@pytest.mark.parametrize("counts", [[256, 257, 383, 384, 385, 511, 512, 1, 128, 129, 0, 130],
+                                    [1, 128, 0, 64, 129, 300, 7, 90]], ids=["large", "small_batch"])
+def test_row_tiles_every_remainder_class(counts):
     """Row-grouped products for experts whose last rows fill a full tile, spill into one
     (remainder > 128 rows) or fit a thin 128-row tile (1..128 rows), plus empty and
-    sub-128-row experts: every row written, each expert's rows equal to its fp64 product."""
-    counts, D, M = [256, 257, 383, 384, 385, 511, 512, 1, 128, 129, 0, 130], 256, 256
+    sub-128-row experts: every row written, each expert's rows equal to its fp64 product.
+    The second case averages under 128 rows per expert, where the down projection's
+    forward also runs thin tiles."""
+    D, M = 256, 256
     o = _operands(counts, D, M, torch.bfloat16, seed=21)
     E, R = o["E"], o["R"]
     s = _lib.stream_of(torch.device("cuda"))
