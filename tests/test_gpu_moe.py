@@ -214,6 +214,21 @@ def test_small_ragged_shapes(T, E, K, rs):
     check_against(moe, x, target, torch.device("cpu"))
 
 
+@pytest.mark.parametrize("T,D,M,E,K", [(50, 72, 200, 5, 2), (130, 136, 264, 12, 3), (300, 192, 320, 3, 1),
+                                        (7, 64, 64, 64, 8), (600, 128, 128, 6, 2)])
+def test_bf16_odd_shapes(T, D, M, E, K):
+    """bf16 layers at sizes the workloads do not reach: D and M multiples of 8 but not of 64
+    (the generic kernel), E = 64 with K = 8 and nearly every expert empty or tiny (thin tiles,
+    the down projection's small-batch path), experts holding full tiles plus a remainder;
+    forward and backward against the oracle."""
+    print(f"\n[moe-bf16-odd] T={T} D={D} M={M} E={E} K={K}", flush=True)
+    torch.manual_seed(T * 7 + D)
+    moe = MoE(dim=D, n_experts=E, top_k=K, hidden_dim=M).to(torch.bfloat16).to(DEV)
+    x = torch.randn(1, T, D, device=DEV).to(torch.bfloat16)
+    target = torch.randn(1, T, D, device=DEV).to(torch.bfloat16)
+    check_against(moe, x, target, torch.device("cpu"))
+
+
 def test_two_training_steps_track_bias_updates():
     """Two train-mode iterations (tests/test_moe_ep.py:49-71): outputs, grads and the bias."""
     torch.manual_seed(1)
