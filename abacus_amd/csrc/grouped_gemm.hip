@@ -1792,10 +1792,14 @@ int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const v
   return dispatch_gemm<kGateUpFwd>(dtype, g, (int)R, (hipStream_t)stream, "gateup_fwd");
 }
 
+// The down projection's forward at small batches: experts average at most
+// THIN rows, so it runs thin tiles (no DMA of padding rows) and no split tail.
+static bool down_fwd_thin(int64_t R, int64_t E) { return R <= (int64_t)pipe::THIN * E; }
+
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype) {
   if (check_gemm_shape(R, D, M, E, dtype) || R == 0) return 0;
   const GemmArgs g = args_down_fwd(nullptr, nullptr, nullptr, R, M, D, E, nullptr);
-  if (!pipe_ok<kDownFwd>(dtype, g)) return 0;
+  if (!pipe_ok<kDownFwd>(dtype, g) || down_fwd_thin(R, E)) return 0;  // no split tail: no workspace
   return plan_split<kDownFwd>(g, (int)R).ws_bytes();
 }
 
@@ -1805,9 +1809,7 @@ int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t*
   if (R == 0) return 0;
   const GemmArgs g = args_down_fwd(h_RM, w_down_EMD, offsets_E1, R, M, D, E, y_RD);
   if (pipe_ok<kDownFwd>(dtype, g)) {
-    // At most THIN rows per expert on average (small batches): thin tiles,
-    // which stream the weights without DMA of padding rows.
-    if (R <= (int64_t)pipe::THIN * E)
+    if (down_fwd_thin(R, E))
       return launch_rows<kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd");
     if (ws != nullptr) {
       const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);

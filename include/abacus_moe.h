@@ -43,7 +43,8 @@ int64_t abacus_moe_hist_len(int64_t T, int64_t E);
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
 /* bytes of the fp32 partial-sum scratch used by router_wgrad. */
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E);
-/* bytes of the split-tail workspace of down_fwd (0: that shape runs no split). */
+/* bytes of the split-tail workspace of down_fwd (0: that shape runs no split, which
+ * includes small batches: R <= 128 * E). */
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype);
 /* bytes of the per-block partial sums and counts used by load_balancing_fwd. */
 int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E);
