@@ -1096,10 +1096,13 @@ int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, con
   if (check_route_shape(T, D, E, K, dtype, false)) return 1;
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
+  ABACUS_CHECK_ARG(wt_ws != nullptr, "unpermute_bwd: router weight workspace is NULL");
   const int EP = e_pad(E);
-  if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
-  else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
-  ABACUS_CHECK_LAUNCH("router weight transpose");
+  if (w_DE != nullptr) {  // else wt_ws already holds router_fwd's transpose of the same weights
+    if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    ABACUS_CHECK_LAUNCH("router weight transpose");
+  }
   if (D % (dtype == kBF16 ? 8 : 4) == 0 && T <= (int64_t)INT_MAX - 3) {
     const unsigned wgrid = (unsigned)((T + 3) / 4);
     if (dtype == kBF16)

@@ -61,7 +61,8 @@ def _contig(t: torch.Tensor) -> torch.Tensor:
 
 
 def _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale):
-    """Launch the fused router; returns (logits, weights, indices, idx32, score, hist)."""
+    """Launch the fused router; returns (logits, weights, indices, idx32, score, hist, wt), wt the
+    transposed router weights the kernel made (the backward's un-permute reuses them)."""
     T, D = x_TD.shape
     E = w_DE.shape[1]
     dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
@@ -76,11 +77,12 @@ def _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale):
         "abacus_moe_router_fwd", ptr(x_TD), ptr(w_DE), ptr(bias_E), T, D, E, top_k, float(route_scale), dt,
         ptr(logits), ptr(weights), ptr(indices), ptr(idx32), ptr(score), ptr(hist), ptr(wt), _lib.stream_of(dev),
     )
-    return logits, weights, indices, idx32, score, hist
+    return logits, weights, indices, idx32, score, hist, wt
 
 
-def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos, dxp):
-    """dx and dW_DE of the router GEMM (plus the un-permute of dxp when given)."""
+def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos, dxp, wt):
+    """dx and dW_DE of the router GEMM (plus the un-permute of dxp when given); wt holds the
+    forward's transposed router weights."""
     T, D = x_TD.shape
     E = w_DE.shape[1]
     K = idx32.shape[1]
@@ -89,9 +91,8 @@ def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos
     dx = dw = None
     if ctx_needs_x:
         dx = torch.empty_like(x_TD)
-        wt = torch.empty(query("abacus_moe_router_ws_bytes", D, E, dt), dtype=torch.uint8, device=dev)
-        call(
-            "abacus_moe_unpermute_bwd", ptr(dxp), ptr(dlogit), ptr(idx32), ptr(pos), ptr(w_DE), ptr(wt),
+        call(  # w_DE = NULL: wt already holds the transposed weights
+            "abacus_moe_unpermute_bwd", ptr(dxp), ptr(dlogit), ptr(idx32), ptr(pos), None, ptr(wt),
             T, D, E, K, dt, ptr(dx), s,
         )
     if ctx_needs_w:
@@ -107,8 +108,8 @@ class _RouterFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x_TD, w_DE, bias_E, top_k, route_scale, record):
-        logits, weights, indices, idx32, score, _ = _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale)
-        ctx.save_for_backward(x_TD, w_DE, weights, score, idx32)
+        logits, weights, indices, idx32, score, _, wt = _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale)
+        ctx.save_for_backward(x_TD, w_DE, weights, score, idx32, wt)
         ctx.route_scale = float(route_scale)
         ctx.mark_non_differentiable(indices)
         if record is not None:
@@ -117,7 +118,7 @@ class _RouterFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dweights, _dindices):
-        x_TD, w_DE, weights, score, idx32 = ctx.saved_tensors
+        x_TD, w_DE, weights, score, idx32, wt = ctx.saved_tensors
         T, K = weights.shape
         dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
         dlogit = torch.empty(T, K, dtype=torch.float32, device=dev)
@@ -127,7 +128,7 @@ class _RouterFunction(torch.autograd.Function):
             ptr(dlogit), _lib.stream_of(dev),
         )
         dx, dw = _router_dgrad_wgrad(
-            ctx.needs_input_grad[0], ctx.needs_input_grad[1], x_TD, w_DE, dlogit, idx32, None, None
+            ctx.needs_input_grad[0], ctx.needs_input_grad[1], x_TD, w_DE, dlogit, idx32, None, None, wt
         )
         return dx, dw, None, None, None, None
 
@@ -143,7 +144,7 @@ class _MoEFunction(torch.autograd.Function):
         R = T * K
         dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
         s = _lib.stream_of(dev)
-        logits, weights, indices, idx32, score, hist = _router_fwd(x_TD, w_DE, bias_E, K, route_scale)
+        logits, weights, indices, idx32, score, hist, wt = _router_fwd(x_TD, w_DE, bias_E, K, route_scale)
         base = torch.empty_like(hist)
         counts = torch.empty(E, dtype=torch.int32, device=dev)
         offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
@@ -170,7 +171,8 @@ class _MoEFunction(torch.autograd.Function):
         out = torch.empty(T, D, dtype=x_TD.dtype, device=dev)
         call("abacus_moe_combine_fwd", ptr(y), ptr(weights), ptr(idx32), ptr(pos), T, D, K, dt, ptr(out), s)
         if need_grad:
-            ctx.save_for_backward(x_TD, w_DE, w_gate, w_up, w_down, xp, gate, up, h, y, weights, score, idx32, pos, offsets)
+            ctx.save_for_backward(x_TD, w_DE, w_gate, w_up, w_down, xp, gate, up, h, y, weights, score, idx32, pos,
+                                  offsets, wt)
         ctx.route_scale = float(route_scale)
         if record is not None:
             record["routing"] = Routing(logits, weights, indices, counts, offsets, perm, pos)
@@ -179,7 +181,7 @@ class _MoEFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         (x_TD, w_DE, w_gate, w_up, w_down, xp, gate, up, h, y, weights, score, idx32, pos,
-         offsets) = ctx.saved_tensors
+         offsets, wt) = ctx.saved_tensors
         T, D = x_TD.shape
         E, _, M = w_gate.shape
         K = idx32.shape[1]
@@ -230,7 +232,7 @@ class _MoEFunction(torch.autograd.Function):
                 "abacus_moe_gateup_bwd_wgrad", ptr(xp), ptr(dgate), ptr(dup), ptr(offsets), R, D, M, E, dt,
                 ptr(dw_gate), ptr(dw_up), s,
             )
-        dx, dw_DE = _router_dgrad_wgrad(needs[0], needs[1], x_TD, w_DE, dlogit, idx32, pos, dxp)
+        dx, dw_DE = _router_dgrad_wgrad(needs[0], needs[1], x_TD, w_DE, dlogit, idx32, pos, dxp, wt)
         return (dx, dw_DE, dw_gate if needs[2] else None, dw_up if needs[3] else None, dw_down,
                 None, None, None, None, None, None)
 

@@ -143,7 +143,9 @@ int abacus_moe_gateup_bwd(const void* dgate_RM, const void* dup_RM, const void* 
 
 /* Backward of the gather of moe.py:77 plus the router GEMM of router.py:45
  * (dgrad): dx[t] = sum_k dx_perm[pos(t,k)] + sum_k dlogit(t,k) w_DE[:, e(t,k)].
- * dx_perm_RD may be NULL (router used on its own). */
+ * dx_perm_RD may be NULL (router used on its own).  wt_ws receives the
+ * transposed router weights; with w_DE NULL it must already hold them, as
+ * abacus_moe_router_fwd left them for the same weights. */
 int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, const int32_t* idx_TK,
                              const int32_t* pos_TK, const void* w_DE, void* wt_ws, int64_t T, int64_t D, int64_t E,
                              int64_t K, int dtype, void* dx_TD, void* stream);
