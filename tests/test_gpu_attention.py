@@ -38,8 +38,11 @@ def _run(q, k, v, scale):
     return o, lse
 
 
-@pytest.mark.parametrize("shape", [(1, 128, 1, 64), (2, 384, 3, 64), (4, 2048, 16, 64)],
-                         ids=["L128", "L384_H3", "decoder"])
+SHAPES = [(1, 128, 1, 64), (2, 384, 3, 64), (3, 1152, 2, 64), (4, 2048, 16, 64)]
+SHAPE_IDS = ["L128", "L384_H3", "L1152_odd_pairs", "decoder"]  # L1152: 9 query blocks, 4 pairs + 1
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=SHAPE_IDS)
 def test_attention_fwd_matches_fp64(shape):
     B, L, H, K = shape
     g = torch.Generator(device="cuda").manual_seed(7)
@@ -71,8 +74,7 @@ def _run_bwd(q, k, v, o, lse2, dout, scale):
     return dq, dk, dv
 
 
-@pytest.mark.parametrize("shape", [(1, 128, 1, 64), (2, 384, 3, 64), (4, 2048, 16, 64)],
-                         ids=["L128", "L384_H3", "decoder"])
+@pytest.mark.parametrize("shape", SHAPES, ids=SHAPE_IDS)
 def test_attention_bwd_matches_fp64(shape):
     B, L, H, K = shape
     g = torch.Generator(device="cuda").manual_seed(11)
