@@ -215,7 +215,8 @@ def test_small_ragged_shapes(T, E, K, rs):
 
 
 @pytest.mark.parametrize("T,D,M,E,K", [(50, 72, 200, 5, 2), (130, 136, 264, 12, 3), (300, 192, 320, 3, 1),
-                                        (7, 64, 64, 64, 8), (600, 128, 128, 6, 2)])
+                                        (7, 64, 64, 64, 8), (600, 128, 128, 6, 2),
+                                        (512, 128, 128, 8, 2), (513, 128, 128, 8, 2)])  # R = 128 E: thin / full
 def test_bf16_odd_shapes(T, D, M, E, K):
     """bf16 layers at sizes the workloads do not reach: D and M multiples of 8 but not of 64
     (the generic kernel), E = 64 with K = 8 and nearly every expert empty or tiny (thin tiles,
