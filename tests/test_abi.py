@@ -50,6 +50,10 @@ def test_abi_version_and_queries():
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 8, _lib.BF16) == 16 * 4096 * 2
     assert _lib.query("abacus_moe_router_ws_bytes", 1024, 17, _lib.F32) == 32 * 1024 * 4
     assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8) > 0
+    # the down projection's split tail needs a workspace at the Mixtral shape, none for small batches
+    assert _lib.query("abacus_moe_down_fwd_ws_bytes", 8192, 14336, 4096, 8, _lib.BF16) > 0
+    assert _lib.query("abacus_moe_down_fwd_ws_bytes", 384, 1408, 2048, 64, _lib.BF16) == 0
+    assert _lib.query("abacus_attention_bwd_ws_bytes", 4, 2048, 16) == 4 * 16 * 2048 * 4
 
 
 @pytest.mark.parametrize(
@@ -61,6 +65,11 @@ def test_abi_version_and_queries():
         ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 2, 1.0, 7) + (None,) * 8, "dtype"),
         ("abacus_moe_gateup_fwd", (None, None, None, None, 16, 64, 30, 8, 0, None, None, None, None), "hidden_dim"),
         ("abacus_moe_down_fwd", (None, None, None, 16, 64, 64, 0, 0, None, None, 0, None), "n_experts"),
+        ("abacus_attention_fwd", (None, None, None, 1, 128, 1, 32, 0.125, 1, None, None, None), "head_dim"),
+        ("abacus_attention_fwd", (None, None, None, 1, 100, 1, 64, 0.125, 1, None, None, None), "multiple of 128"),
+        ("abacus_attention_fwd", (None, None, None, 1, 128, 1, 64, 0.125, 0, None, None, None), "bf16 only"),
+        ("abacus_cross_entropy_fwd", (None, None, 4, 10, -100, 5, None, None, None), "dtype"),
+        ("abacus_cross_entropy_bwd", (None, None, None, None, 1.0, 4, 0, -100, 1, None, None), "bad shape"),
     ],
 )
 def test_rejected_arguments_raise_with_message(name, args, msg):
