@@ -250,3 +250,7 @@ def test_liger_cross_entropy_matches_torch_on_gpu():
     assert abs(float(loss.detach()) - float(ref.detach())) <= 2 ** -8 * abs(float(ref.detach()))
     assert float((grad.double() - ref_grad).norm() / ref_grad.norm()) < 4e-3
     assert torch.isnan(cross_entropy(x.detach(), torch.full_like(t, -100)))
+    # options the kernels do not take go to torch's cross_entropy unchanged
+    xd = x.detach()
+    for kw in ({"label_smoothing": 0.1}, {"reduction": "sum"}, {"reduction": "none"}):
+        torch.testing.assert_close(cross_entropy(xd, t, **kw), F.cross_entropy(xd, t, **kw), rtol=0, atol=0)
