@@ -16,6 +16,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "libabacus_moe.so"
 
 F32 = 0
 BF16 = 1
+TILE_CTR_INTS = 16  # ABACUS_MOE_TILE_CTR_INTS
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -45,11 +46,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_combine_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_moe_combine_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P]),
     "abacus_moe_down_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
-    "abacus_moe_down_bwd_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
+    "abacus_moe_down_bwd_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
     "abacus_moe_gateup_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
-    "abacus_moe_gateup_bwd_wgrad": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
-    "abacus_moe_down_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
-    "abacus_moe_gateup_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
+    "abacus_moe_gateup_bwd_wgrad": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
+    "abacus_moe_down_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P]),
+    "abacus_moe_gateup_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P]),
     "abacus_moe_unpermute_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_moe_router_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
     "abacus_router_gating_bwd": (_I, [_P, _P, _P, _I64, _I64, _F, _I, _P, _P]),
@@ -164,6 +165,11 @@ def ptr(t: torch.Tensor | None) -> int | None:
     if p % 16 != 0 and t.numel() > 0:
         raise ValueError("kernel operands must be 16-byte aligned")
     return p
+
+
+def tile_ctr(device: torch.device) -> torch.Tensor:
+    """Tile-counter workspace of one weight-gradient call (the call clears it on its stream)."""
+    return torch.empty(TILE_CTR_INTS, dtype=torch.int32, device=device)
 
 
 def stream_of(device: torch.device) -> int:

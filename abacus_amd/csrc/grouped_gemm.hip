@@ -51,6 +51,10 @@ template <> struct KindTraits<kGateUpDgrad> { static constexpr bool A_MC = false
 template <> struct KindTraits<kDownWgrad> { static constexpr bool A_MC = true, B_NC = true, DUAL_B = false, DUAL_K = false, WGRAD = true; };
 template <> struct KindTraits<kGateUpWgrad> { static constexpr bool A_MC = true, B_NC = true, DUAL_B = true, DUAL_K = false, WGRAD = true; };
 
+// Tile counters of a persistent weight-gradient launch (caller workspace).
+constexpr int kTileCtrInts = ABACUS_MOE_TILE_CTR_INTS;
+static_assert(kTileCtrInts >= 8, "one counter per XCD");
+
 struct GemmArgs {
   const void* a0;
   const void* a1;
@@ -83,9 +87,10 @@ struct GemmArgs {
   // Pipelined kernel, row-grouped kinds: nonzero when expert remainders of at
   // most THIN rows go to thin tiles (else every row tile is a full one).
   int thin;
-  // Pipelined kernel, weight gradients: this launch's set of tile counters
-  // (pipe::g_tile_ctr).
-  int ctr_slot;
+  // Pipelined kernel, weight gradients: this launch's tile counters, in the
+  // caller's workspace (kTileCtrInts ints), zeroed on the stream right before
+  // the launch: [c] is the next unclaimed tile of XCD c's share.
+  int* tile_ctr;
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -1096,15 +1101,19 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 // issues the next tile's first DMA before the finished tile's stores, so the
 // DMA latency and the stores overlap.
 //
-// Counters: one set per launch slot.  The host gives consecutive launches
-// consecutive slots, so launches in flight on different streams use different
-// counters; the last of a launch's P blocks to finish sets its slot back to
-// zero for the next launch that uses it.
-constexpr int kCtrSlots = 64;
+// Counters: eight per launch, in memory the caller passes (GemmArgs::tile_ctr)
+// and ctr_zero_kernel clears on the launch's stream just before it; so no
+// state outlives a launch, and launches in flight on several streams (or
+// replayed from a captured graph) each count in their own memory.
 // The expert offsets a block keeps in LDS (check_gemm_shape's bound); with
 // the thin tiles' 144 KB ring the pair launches then stay within 160 KB.
 constexpr int kMaxExperts = 1024;
-__device__ int g_tile_ctr[kCtrSlots][16] = {};  // [0..7] next tile of each XCD's share, [8] blocks done
+
+// Clears a launch's tile counters (a kernel, not a memset, so that a captured
+// graph replays it as a kernel node).
+__global__ void ctr_zero_kernel(int* ctr) {
+  if (threadIdx.x < kTileCtrInts) ctr[threadIdx.x] = 0;
+}
 
 __device__ inline int xcc_id() { return __builtin_amdgcn_s_getreg((31 << 11) | 20) & 7; }  // HW_REG_XCC_ID
 
@@ -1127,7 +1136,7 @@ __device__ inline int claim_tile(int* ctr, int xcc, int& from, int per, int tota
 // one int; offs_s, kMaxExperts + 1 ints (the expert offsets, so that starting
 // a tile waits on no global load).
 template <int KIND>
-__device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const GemmArgs& g, int P, char* lds,
+__device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const GemmArgs& g, char* lds,
                                                                        int* next_s, int* offs_s) {
   using KT = KindTraits<KIND>;
   using Op = MfmaOp<uint16_t, 32>;
@@ -1156,7 +1165,7 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
     wave_u = __builtin_amdgcn_readfirstlane(wave);
   };
 
-  int* ctr = g_tile_ctr[g.ctr_slot];
+  int* ctr = g.tile_ctr;
   const int total = g.E * g.tiles_m * g.tiles_n;  // logical tiles, padding included
   const int per = (total + 7) / 8;
   const int xcc = xcc_id();
@@ -1342,11 +1351,6 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
     L = Ln;
   }
 
-  // the last block out sets the counters back to zero
-  if (tid == 0 && atomicAdd(&ctr[8], 1) == P - 1) {
-#pragma unroll
-    for (int c = 0; c < 9; ++c) atomicExch(&ctr[c], 0);
-  }
 }
 
 template <int KIND>
@@ -1354,7 +1358,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_wgrad_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_ALLOC];
   __shared__ int next_s;
   __shared__ int offs_s[kMaxExperts + 1];
-  gemm_wgrad_tiles<KIND>(g, (int)gridDim.x, lds, &next_s, offs_s);
+  gemm_wgrad_tiles<KIND>(g, lds, &next_s, offs_s);
 }
 
 // A row-grouped kind's full tiles, then its thin tiles, then (KW >= 0) a
@@ -1376,7 +1380,7 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, Gemm
     if constexpr (KW >= 0) {
       __shared__ int next_s;
       __shared__ int offs_s[kMaxExperts + 1];
-      gemm_wgrad_tiles<KW>(g3, (int)gridDim.x - n1 - n2, lds, &next_s, offs_s);
+      gemm_wgrad_tiles<KW>(g3, lds, &next_s, offs_s);
     }
   }
 }
@@ -1478,23 +1482,15 @@ int64_t pipe_grid(GemmArgs& g, int R) {
   return (int64_t)(KT::WGRAD ? g.E : 1) * g.tiles_m * g.tiles_n;
 }
 
-// Counter slot of a persistent weight-gradient launch: consecutive launches
-// take consecutive slots.
-inline int next_ctr_slot() {
-  static std::atomic<unsigned> seq{0};
-  return (int)(seq.fetch_add(1, std::memory_order_relaxed) % pipe::kCtrSlots);
-}
-
 inline int cu_count();
 
 // Blocks of a persistent weight-gradient launch (one per CU, at most one per
-// tile); sizes its tile space and takes its counter slot.  0: no tiles.
+// tile); sizes its tile space.  0: no tiles.
 template <int KIND>
 int64_t wgrad_blocks(GemmArgs& g, int R) {
   static_assert(KindTraits<KIND>::WGRAD, "weight-gradient kinds");
   const int64_t total = pipe_grid<KIND>(g, R);
   if (total == 0) return 0;
-  g.ctr_slot = next_ctr_slot();
   return std::min<int64_t>(cu_count(), total);
 }
 
@@ -1527,6 +1523,11 @@ int launch_rows(const GemmArgs& g1, int R, const GemmArgs* gw, int64_t n1, bool 
   }
   ABACUS_CHECK_ARG(n1 + n2 + n3 < (1ll << 31), "%s: tile grid too large", name);
   if (n1 + n2 + n3 == 0) return 0;
+  if (n3 > 0) {
+    ABACUS_CHECK_ARG(gc.tile_ctr != nullptr, "%s: tile_ctr workspace is NULL", name);
+    hipLaunchKernelGGL(pipe::ctr_zero_kernel, dim3(1), dim3(64), 0, s, gc.tile_ctr);
+    ABACUS_CHECK_LAUNCH(name);
+  }
   hipLaunchKernelGGL((pipe::gemm_bf16_rows_kernel<KR, KW>), dim3((unsigned)(n1 + n2 + n3)), dim3(pipe::NT), 0, s, ga,
                      gt, gc, (int)n1, (int)n2);
   ABACUS_CHECK_LAUNCH(name);
@@ -1544,6 +1545,9 @@ int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
     const int64_t blocks = wgrad_blocks<KIND>(ga, R);
     if (blocks == 0) return 0;
     ABACUS_CHECK_ARG((int64_t)ga.E * ga.tiles_m * ga.tiles_n < (1ll << 31), "%s: tile grid too large", name);
+    ABACUS_CHECK_ARG(ga.tile_ctr != nullptr, "%s: tile_ctr workspace is NULL", name);
+    hipLaunchKernelGGL(pipe::ctr_zero_kernel, dim3(1), dim3(64), 0, s, ga.tile_ctr);
+    ABACUS_CHECK_LAUNCH(name);
     hipLaunchKernelGGL(pipe::gemm_bf16_wgrad_kernel<KIND>, dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
     ABACUS_CHECK_LAUNCH(name);
     return 0;
@@ -1830,18 +1834,23 @@ int abacus_moe_down_bwd_dgrad(const void* dy_RD, const void* w_down_EMD, const v
 }
 
 int abacus_moe_down_bwd_wgrad(const void* h_RM, const void* dy_RD, const int32_t* offsets_E1, int64_t R, int64_t M,
-                              int64_t D, int64_t E, int dtype, void* dw_down_EMD, void* stream) {
+                              int64_t D, int64_t E, int dtype, void* dw_down_EMD, int32_t* tile_ctr, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
-  const GemmArgs g = args_down_wgrad(h_RM, dy_RD, offsets_E1, M, D, E, dw_down_EMD);
+  GemmArgs g = args_down_wgrad(h_RM, dy_RD, offsets_E1, M, D, E, dw_down_EMD);
+  g.tile_ctr = tile_ctr;
+  ABACUS_CHECK_ARG(tile_ctr != nullptr, "tile_ctr workspace is NULL");
   return dispatch_gemm<kDownWgrad>(dtype, g, (int)R, (hipStream_t)stream, "down_bwd_wgrad");
 }
 
 int abacus_moe_down_bwd(const void* dy_RD, const void* w_down_EMD, const void* gate_RM, const void* up_RM,
                         const void* h_RM, const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E,
-                        int dtype, void* dgate_RM, void* dup_RM, void* dw_down_EMD, void* stream) {
+                        int dtype, void* dgate_RM, void* dup_RM, void* dw_down_EMD, int32_t* tile_ctr,
+                        void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   const GemmArgs gd = args_down_dgrad(dy_RD, w_down_EMD, gate_RM, up_RM, offsets_E1, R, M, D, E, dgate_RM, dup_RM);
-  const GemmArgs gw = args_down_wgrad(h_RM, dy_RD, offsets_E1, M, D, E, dw_down_EMD);
+  GemmArgs gw = args_down_wgrad(h_RM, dy_RD, offsets_E1, M, D, E, dw_down_EMD);
+  gw.tile_ctr = tile_ctr;
+  ABACUS_CHECK_ARG(tile_ctr != nullptr, "tile_ctr workspace is NULL");
   return dispatch_pair<kDownDgrad, kDownWgrad>(dtype, gd, gw, (int)R, (hipStream_t)stream, "down_bwd_dgrad",
                                                "down_bwd_wgrad", "down_bwd");
 }
@@ -1857,18 +1866,23 @@ int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const 
 
 int abacus_moe_gateup_bwd_wgrad(const void* x_perm_RD, const void* dgate_RM, const void* dup_RM,
                                 const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
-                                void* dw_gate_EDM, void* dw_up_EDM, void* stream) {
+                                void* dw_gate_EDM, void* dw_up_EDM, int32_t* tile_ctr, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
-  const GemmArgs g = args_gateup_wgrad(x_perm_RD, dgate_RM, dup_RM, offsets_E1, D, M, E, dw_gate_EDM, dw_up_EDM);
+  GemmArgs g = args_gateup_wgrad(x_perm_RD, dgate_RM, dup_RM, offsets_E1, D, M, E, dw_gate_EDM, dw_up_EDM);
+  g.tile_ctr = tile_ctr;
+  ABACUS_CHECK_ARG(tile_ctr != nullptr, "tile_ctr workspace is NULL");
   return dispatch_gemm<kGateUpWgrad>(dtype, g, (int)R, (hipStream_t)stream, "gateup_bwd_wgrad");
 }
 
 int abacus_moe_gateup_bwd(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM, const void* w_up_EDM,
                           const void* x_perm_RD, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
-                          int64_t E, int dtype, void* dx_perm_RD, void* dw_gate_EDM, void* dw_up_EDM, void* stream) {
+                          int64_t E, int dtype, void* dx_perm_RD, void* dw_gate_EDM, void* dw_up_EDM,
+                          int32_t* tile_ctr, void* stream) {
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   const GemmArgs gd = args_gateup_dgrad(dgate_RM, dup_RM, w_gate_EDM, w_up_EDM, offsets_E1, R, D, M, E, dx_perm_RD);
-  const GemmArgs gw = args_gateup_wgrad(x_perm_RD, dgate_RM, dup_RM, offsets_E1, D, M, E, dw_gate_EDM, dw_up_EDM);
+  GemmArgs gw = args_gateup_wgrad(x_perm_RD, dgate_RM, dup_RM, offsets_E1, D, M, E, dw_gate_EDM, dw_up_EDM);
+  gw.tile_ctr = tile_ctr;
+  ABACUS_CHECK_ARG(tile_ctr != nullptr, "tile_ctr workspace is NULL");
   return dispatch_pair<kGateUpDgrad, kGateUpWgrad>(dtype, gd, gw, (int)R, (hipStream_t)stream, "gateup_bwd_dgrad",
                                                    "gateup_bwd_wgrad", "gateup_bwd");
 }

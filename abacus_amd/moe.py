@@ -205,7 +205,7 @@ class _MoEFunction(torch.autograd.Function):
             dw_down = torch.empty_like(w_down)
             call(
                 "abacus_moe_down_bwd", ptr(dy), ptr(w_down), ptr(gate), ptr(up), ptr(h), ptr(offsets), R, M, D, E,
-                dt, ptr(dgate), ptr(dup), ptr(dw_down), s,
+                dt, ptr(dgate), ptr(dup), ptr(dw_down), ptr(_lib.tile_ctr(dev)), s,
             )
         else:
             call(
@@ -220,7 +220,7 @@ class _MoEFunction(torch.autograd.Function):
         if dxp is not None and dw_gate is not None:
             call(
                 "abacus_moe_gateup_bwd", ptr(dgate), ptr(dup), ptr(w_gate), ptr(w_up), ptr(xp), ptr(offsets),
-                R, D, M, E, dt, ptr(dxp), ptr(dw_gate), ptr(dw_up), s,
+                R, D, M, E, dt, ptr(dxp), ptr(dw_gate), ptr(dw_up), ptr(_lib.tile_ctr(dev)), s,
             )
         elif dxp is not None:
             call(
@@ -230,7 +230,7 @@ class _MoEFunction(torch.autograd.Function):
         elif dw_gate is not None:
             call(
                 "abacus_moe_gateup_bwd_wgrad", ptr(xp), ptr(dgate), ptr(dup), ptr(offsets), R, D, M, E, dt,
-                ptr(dw_gate), ptr(dw_up), s,
+                ptr(dw_gate), ptr(dw_up), ptr(_lib.tile_ctr(dev)), s,
             )
         dx, dw_DE = _router_dgrad_wgrad(needs[0], needs[1], x_TD, w_DE, dlogit, idx32, pos, dxp, wt)
         return (dx, dw_DE, dw_gate if needs[2] else None, dw_up if needs[3] else None, dw_down,

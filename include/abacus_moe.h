@@ -34,6 +34,12 @@ extern "C" {
 
 enum { ABACUS_F32 = 0, ABACUS_BF16 = 1 };
 
+/* int32 elements of the tile-counter workspace (tile_ctr) that the weight-gradient
+ * entry points take: device memory the call clears on its stream and then uses
+ * for the launch's work counters.  Calls in flight at the same time need
+ * separate workspaces; its contents after the call are unspecified. */
+#define ABACUS_MOE_TILE_CTR_INTS 16
+
 /* ---- library / sizing queries ------------------------------------------ */
 const char* abacus_moe_last_error(void);
 int abacus_moe_abi_version(void);
@@ -112,34 +118,38 @@ int abacus_moe_down_bwd_dgrad(const void* dy_RD, const void* w_down_EMD, const v
                               const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E, int dtype,
                               void* dgate_RM, void* dup_RM, void* stream);
 
-/* Backward of moe.py:80 (wgrad): dw_down[e] = h_e^T dy_e; zero for empty experts. */
+/* Backward of moe.py:80 (wgrad): dw_down[e] = h_e^T dy_e; zero for empty experts.
+ * tile_ctr: ABACUS_MOE_TILE_CTR_INTS ints of workspace. */
 int abacus_moe_down_bwd_wgrad(const void* h_RM, const void* dy_RD, const int32_t* offsets_E1, int64_t R, int64_t M,
-                              int64_t D, int64_t E, int dtype, void* dw_down_EMD, void* stream);
+                              int64_t D, int64_t E, int dtype, void* dw_down_EMD, int32_t* tile_ctr, void* stream);
 
 /* Backward of moe.py:80, both halves in one launch: abacus_moe_down_bwd_dgrad
  * and abacus_moe_down_bwd_wgrad on the same operands (the weight gradient's
  * short per-expert tiles fill the CUs the data gradient's last round leaves
- * idle).  Outputs are those two calls' outputs, bit for bit. */
+ * idle).  Outputs are those two calls' outputs, bit for bit.  tile_ctr: as above. */
 int abacus_moe_down_bwd(const void* dy_RD, const void* w_down_EMD, const void* gate_RM, const void* up_RM,
                         const void* h_RM, const int32_t* offsets_E1, int64_t R, int64_t M, int64_t D, int64_t E,
-                        int dtype, void* dgate_RM, void* dup_RM, void* dw_down_EMD, void* stream);
+                        int dtype, void* dgate_RM, void* dup_RM, void* dw_down_EMD, int32_t* tile_ctr,
+                        void* stream);
 
 /* Backward of moe.py:78-79 (dgrad): dx_perm = dgate @ w_gate[e]^T + dup @ w_up[e]^T. */
 int abacus_moe_gateup_bwd_dgrad(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM,
                                 const void* w_up_EDM, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
                                 int64_t E, int dtype, void* dx_perm_RD, void* stream);
 
-/* Backward of moe.py:78-79 (wgrad): dw_gate[e] = x_e^T dgate_e, dw_up[e] = x_e^T dup_e. */
+/* Backward of moe.py:78-79 (wgrad): dw_gate[e] = x_e^T dgate_e, dw_up[e] = x_e^T dup_e.
+ * tile_ctr: ABACUS_MOE_TILE_CTR_INTS ints of workspace. */
 int abacus_moe_gateup_bwd_wgrad(const void* x_perm_RD, const void* dgate_RM, const void* dup_RM,
                                 const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
-                                void* dw_gate_EDM, void* dw_up_EDM, void* stream);
+                                void* dw_gate_EDM, void* dw_up_EDM, int32_t* tile_ctr, void* stream);
 
 /* Backward of moe.py:78-79, both halves in one launch: abacus_moe_gateup_bwd_dgrad
  * and abacus_moe_gateup_bwd_wgrad on the same operands.  Outputs are those two
- * calls' outputs, bit for bit. */
+ * calls' outputs, bit for bit.  tile_ctr: as above. */
 int abacus_moe_gateup_bwd(const void* dgate_RM, const void* dup_RM, const void* w_gate_EDM, const void* w_up_EDM,
                           const void* x_perm_RD, const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M,
-                          int64_t E, int dtype, void* dx_perm_RD, void* dw_gate_EDM, void* dw_up_EDM, void* stream);
+                          int64_t E, int dtype, void* dx_perm_RD, void* dw_gate_EDM, void* dw_up_EDM,
+                          int32_t* tile_ctr, void* stream);
 
 /* Backward of the gather of moe.py:77 plus the router GEMM of router.py:45
  * (dgrad): dx[t] = sum_k dx_perm[pos(t,k)] + sum_k dlogit(t,k) w_DE[:, e(t,k)].

@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_queries():
     lib = _lib.load()
-    assert lib.abacus_moe_abi_version() == 1
+    assert lib.abacus_moe_abi_version() == 2
     assert _lib.query("abacus_moe_hist_len", 4096, 8) == (4096 // 16) * 8
     assert _lib.query("abacus_moe_hist_len", 17, 8) == 2 * 8
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 8, _lib.BF16) == 16 * 4096 * 2
@@ -70,6 +70,9 @@ def test_abi_version_and_queries():
         ("abacus_attention_fwd", (None, None, None, 1, 128, 1, 64, 0.125, 0, None, None, None), "bf16 only"),
         ("abacus_cross_entropy_fwd", (None, None, 4, 10, -100, 5, None, None, None), "dtype"),
         ("abacus_cross_entropy_bwd", (None, None, None, None, 1.0, 4, 0, -100, 1, None, None), "bad shape"),
+        ("abacus_moe_gateup_bwd_wgrad", (None, None, None, None, 16, 64, 64, 8, 1, None, None, None, None),
+         "tile_ctr"),
+        ("abacus_moe_down_bwd", (None,) * 6 + (16, 64, 64, 8, 1) + (None,) * 5, "tile_ctr"),
     ],
 )
 def test_rejected_arguments_raise_with_message(name, args, msg):

@@ -69,3 +69,20 @@ def test_next_token_loss_uses_kernels_and_matches_slice_form():
     err = float((grad.double() - ref_grad).norm() / ref_grad.norm())
     assert err < 4e-3, err
     assert torch.count_nonzero(grad[:, -1]) == 0
+
+
+@pytest.mark.parametrize("bad", [32000, -3], ids=["past_vocab", "negative"])
+def test_cross_entropy_rejects_out_of_range_targets(bad):
+    """kernels/liger.py:12-47 on GPU logits: a target outside [0, V) other than ignore_index raises
+    IndexError before any launch (torch's CPU cross_entropy raises too), instead of a mean over the
+    other rows."""
+    from abacus_amd.train import cross_entropy
+
+    logits, targets = _case(64, 32000, torch.bfloat16, seed=9)
+    targets[5] = bad
+    timer = _lib.KernelTimer()
+    with timer, pytest.raises(IndexError, match=str(bad)):
+        cross_entropy(logits, targets)
+    assert not timer.totals_ms()
+    targets[5] = -100  # the ignore index itself is fine
+    assert torch.isfinite(cross_entropy(logits, targets))

@@ -49,7 +49,8 @@ CASES = [
 def test_down_bwd_pair_equals_separate_calls(dtype, counts, D, M):
     o = _operands(counts, D, M, dtype, seed=11)
     E, R, dt = o["E"], o["R"], _lib.dtype_code(dtype)
-    s = _lib.stream_of(torch.device("cuda"))
+    dev = torch.device("cuda")
+    s = _lib.stream_of(dev)
     out = {}
     for mode in ("pair", "single"):
         dg = torch.full((R, M), float("nan"), dtype=dtype, device="cuda")
@@ -57,12 +58,12 @@ def test_down_bwd_pair_equals_separate_calls(dtype, counts, D, M):
         dwd = torch.full((E, M, D), float("nan"), dtype=dtype, device="cuda")
         if mode == "pair":
             call("abacus_moe_down_bwd", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]), ptr(o["h"]),
-                 ptr(o["offsets"]), R, M, D, E, dt, ptr(dg), ptr(du), ptr(dwd), s)
+                 ptr(o["offsets"]), R, M, D, E, dt, ptr(dg), ptr(du), ptr(dwd), ptr(_lib.tile_ctr(dev)), s)
         else:
             call("abacus_moe_down_bwd_dgrad", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]),
                  ptr(o["offsets"]), R, M, D, E, dt, ptr(dg), ptr(du), s)
             call("abacus_moe_down_bwd_wgrad", ptr(o["h"]), ptr(o["dy"]), ptr(o["offsets"]), R, M, D, E, dt,
-                 ptr(dwd), s)
+                 ptr(dwd), ptr(_lib.tile_ctr(dev)), s)
         out[mode] = (dg, du, dwd)
     torch.cuda.synchronize()
     for a, b, name in zip(out["pair"], out["single"], ("dgate", "dup", "dw_down")):
@@ -79,7 +80,8 @@ def test_down_bwd_pair_equals_separate_calls(dtype, counts, D, M):
 def test_gateup_bwd_pair_equals_separate_calls(dtype, counts, D, M):
     o = _operands(counts, D, M, dtype, seed=12)
     E, R, dt = o["E"], o["R"], _lib.dtype_code(dtype)
-    s = _lib.stream_of(torch.device("cuda"))
+    dev = torch.device("cuda")
+    s = _lib.stream_of(dev)
     out = {}
     for mode in ("pair", "single"):
         dx = torch.full((R, D), float("nan"), dtype=dtype, device="cuda")
@@ -87,12 +89,13 @@ def test_gateup_bwd_pair_equals_separate_calls(dtype, counts, D, M):
         dwu = torch.full((E, D, M), float("nan"), dtype=dtype, device="cuda")
         if mode == "pair":
             call("abacus_moe_gateup_bwd", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]),
-                 ptr(o["xp"]), ptr(o["offsets"]), R, D, M, E, dt, ptr(dx), ptr(dwg), ptr(dwu), s)
+                 ptr(o["xp"]), ptr(o["offsets"]), R, D, M, E, dt, ptr(dx), ptr(dwg), ptr(dwu),
+                 ptr(_lib.tile_ctr(dev)), s)
         else:
             call("abacus_moe_gateup_bwd_dgrad", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]),
                  ptr(o["offsets"]), R, D, M, E, dt, ptr(dx), s)
             call("abacus_moe_gateup_bwd_wgrad", ptr(o["xp"]), ptr(o["dgate"]), ptr(o["dup"]), ptr(o["offsets"]),
-                 R, D, M, E, dt, ptr(dwg), ptr(dwu), s)
+                 R, D, M, E, dt, ptr(dwg), ptr(dwu), ptr(_lib.tile_ctr(dev)), s)
         out[mode] = (dx, dwg, dwu)
     torch.cuda.synchronize()
     for a, b, name in zip(out["pair"], out["single"], ("dx_perm", "dw_gate", "dw_up")):
@@ -114,7 +117,7 @@ def test_pair_results_match_fp64_products():
     dwg = torch.empty(E, D, M, dtype=torch.bfloat16, device="cuda")
     dwu = torch.empty(E, D, M, dtype=torch.bfloat16, device="cuda")
     call("abacus_moe_gateup_bwd", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["xp"]),
-         ptr(o["offsets"]), R, D, M, E, 1, ptr(dx), ptr(dwg), ptr(dwu), s)
+         ptr(o["offsets"]), R, D, M, E, 1, ptr(dx), ptr(dwg), ptr(dwu), ptr(_lib.tile_ctr(torch.device("cuda"))), s)
     torch.cuda.synchronize()
     off = o["offsets"].tolist()
     f = lambda t: t.double().cpu()
@@ -220,24 +223,31 @@ WGRAD_CASES = [
 ]
 
 
-def _wgrads(o, D, M, s, out=None):
-    """Both weight gradients through the single entry points (persistent tile loop), into `out` or new buffers."""
+def _wgrads(o, D, M, s, out=None, ctrs=None):
+    """Both weight gradients through the single entry points (persistent tile loop), into `out` or new buffers.
+
+    ctrs: the two calls' tile-counter workspaces (fresh ones when None); the caller keeps them alive
+    until the calls are done."""
     E, R = o["E"], o["R"]
     if out is None:
         out = tuple(torch.full(shape, float("nan"), dtype=torch.bfloat16, device="cuda")
                     for shape in ((E, M, D), (E, D, M), (E, D, M)))
+    if ctrs is None:
+        ctrs = (_lib.tile_ctr(torch.device("cuda")), _lib.tile_ctr(torch.device("cuda")))
     dwd, dwg, dwu = out
-    call("abacus_moe_down_bwd_wgrad", ptr(o["h"]), ptr(o["dy"]), ptr(o["offsets"]), R, M, D, E, 1, ptr(dwd), s)
+    call("abacus_moe_down_bwd_wgrad", ptr(o["h"]), ptr(o["dy"]), ptr(o["offsets"]), R, M, D, E, 1, ptr(dwd),
+         ptr(ctrs[0]), s)
     call("abacus_moe_gateup_bwd_wgrad", ptr(o["xp"]), ptr(o["dgate"]), ptr(o["dup"]), ptr(o["offsets"]), R, D, M, E,
-         1, ptr(dwg), ptr(dwu), s)
+         1, ptr(dwg), ptr(dwu), ptr(ctrs[1]), s)
     return out
 
 
 @pytest.mark.parametrize("counts,D,M", WGRAD_CASES, ids=["few_tiles", "many_tiles"])
 def test_wgrad_tile_loop(counts, D, M):
     """Weight gradients from the persistent tile loop: each expert's product (fp64 truth), exact
-    zeros for experts without rows, bit-identical results over more launches than there are
-    counter slots (each launch's counters must be left at zero), and on two streams at once."""
+    zeros for experts without rows, bit-identical results over 70 launches that reuse one
+    counter workspace left dirty by the previous launch (or filled with junk: each call clears
+    its own), and with launches in flight on two streams at once, each with its own workspace."""
     o = _operands(counts, D, M, torch.bfloat16, seed=31)
     dev = torch.device("cuda")
     s = _lib.stream_of(dev)
@@ -258,21 +268,26 @@ def test_wgrad_tile_loop(counts, D, M):
                                 (first[2][e], f(o["xp"][a:b]).T @ f(o["dup"][a:b]), "dw_up")):
             err = float((f(got) - want).norm() / want.norm())
             assert err < 1e-2, f"expert {e} {name}: relative error {err:.3g}"
-    # 70 launches of each kind on one stream (more than the 64 counter slots), same buffers
+    # 70 launches of each kind on one stream, same buffers and the same two counter workspaces
     again = tuple(torch.empty_like(t) for t in first)
+    ctrs = (_lib.tile_ctr(dev), _lib.tile_ctr(dev))
     for i in range(70):
         for t in again:
             t.fill_(float("nan"))
-        _wgrads(o, D, M, s, again)
+        if i % 10 == 0:
+            for c in ctrs:
+                c.fill_(123456 if i % 20 == 0 else -7)
+        _wgrads(o, D, M, s, again, ctrs)
         torch.cuda.synchronize()
         for a, b, name in zip(first, again, ("dw_down", "dw_gate", "dw_up")):
             assert torch.equal(a, b), f"launch {i + 1}: {name} differs"
     # two streams (default priority) with launches in flight on both at once
     streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
     outs = [tuple(torch.full_like(t, float("nan")) for t in first) for _ in range(6)]
+    wss = [(_lib.tile_ctr(dev), _lib.tile_ctr(dev)) for _ in outs]
     torch.cuda.synchronize()
     for i, out in enumerate(outs):
-        _wgrads(o, D, M, streams[i % 2].cuda_stream, out)
+        _wgrads(o, D, M, streams[i % 2].cuda_stream, out, wss[i])
     torch.cuda.synchronize()
     for i, out in enumerate(outs):
         for a, b, name in zip(first, out, ("dw_down", "dw_gate", "dw_up")):
