@@ -53,6 +53,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_gateup_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P]),
     "abacus_moe_unpermute_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_moe_router_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
+    "abacus_moe_router_wgrad_noalloc": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_router_gating_bwd": (_I, [_P, _P, _P, _I64, _I64, _F, _I, _P, _P]),
     "abacus_router_update_bias": (_I, [_P, _I64, _I64, _F, _I, _P, _P]),
     "abacus_rmsnorm_fwd": (_I, [_P, _P, _I64, _I64, _F, _I, _P, _P, _P]),

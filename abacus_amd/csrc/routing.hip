@@ -14,6 +14,7 @@
 #include <algorithm>
 
 #include <climits>
+#include <mutex>
 
 #include "common.h"
 
@@ -949,6 +950,40 @@ void launch_transpose(const void* w, void* wt, int D, int E, int E_pad, hipStrea
 
 inline int e_pad(int64_t E) { return (int)((E + 15) / 16) * 16; }
 
+// The allocation-free router weight gradient's partial sums: a static device
+// array, one copy per GPU, held until the process ends.  Host code must never
+// pass `scratch` itself to a kernel (its host-side name is only a handle):
+// scratch_ptr() looks up this GPU's address of it once per device, with that
+// device current, and every launch takes that address.  Calls that overlap on
+// one GPU share the array and race.
+constexpr int64_t kScratchBytes = 32ll << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_dev[kMaxScratchDevices] = {};
+
+// This device's address of `scratch` (nullptr, with the error set, on failure).
+float* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("router_wgrad_noalloc: no current HIP device (or device index beyond %d)", kMaxScratchDevices - 1);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || p == nullptr) {
+      set_error("router_wgrad_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(rc));
+      return nullptr;
+    }
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  return g_scratch_dev[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -1160,12 +1195,8 @@ int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E) {
   return best;
 }
 
-int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
-                            int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream) {
-  if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
-  ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
-  hipStream_t s = (hipStream_t)stream;
+static int router_wgrad_launch(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
+                               int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, hipStream_t s) {
   const bool reg = router_wgrad_reg_path(D, E, dtype);
   int chunk, nchunks;
   router_wgrad_plan(T, D, E, dtype, reg, &chunk, &nchunks);
@@ -1213,6 +1244,34 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
   }
   ABACUS_CHECK_LAUNCH("router_wgrad_reduce");
   return 0;
+}
+
+static int check_router_wgrad(int64_t E, int64_t K, int dtype) {
+  if (check_dtype(dtype)) return 1;
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
+  return 0;
+}
+
+int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
+                            int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream) {
+  if (check_router_wgrad(E, K, dtype)) return 1;
+  return router_wgrad_launch(x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype, partial_ws, dw_DE, (hipStream_t)stream);
+}
+
+int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T,
+                                    int64_t D, int64_t E, int64_t K, int dtype, void* dw_DE, void* stream) {
+  if (check_router_wgrad(E, K, dtype)) return 1;
+  int chunk, nchunks;
+  router_wgrad_plan(T, D, E, dtype, router_wgrad_reg_path(D, E, dtype), &chunk, &nchunks);
+  const int64_t need = (int64_t)nchunks * E * D * (int64_t)sizeof(float);
+  ABACUS_CHECK_ARG(need <= kScratchBytes,
+                   "router_wgrad_noalloc: T=%lld D=%lld E=%lld needs %lld bytes of partial sums, more than the "
+                   "library's %lld-byte static scratch; call abacus_moe_router_wgrad with a workspace",
+                   (long long)T, (long long)D, (long long)E, (long long)need, (long long)kScratchBytes);
+  float* partial = scratch_ptr();
+  if (partial == nullptr) return 2;
+  return router_wgrad_launch(x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype, partial, dw_DE, (hipStream_t)stream);
 }
 
 int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, float speed, int dtype, void* bias_E,

@@ -164,6 +164,16 @@ int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, con
 int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
                             int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream);
 
+/* No counterpart in the reference: abacus_moe_router_wgrad for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  The same kernels and the same result bit for bit, with the partial
+ * sums in a static 32 MiB device array of the library (one per GPU, held until the
+ * process ends) instead of partial_ws.  Shapes whose partial sums need more than
+ * 32 MiB are rejected (1) before any launch; abacus_moe_router_wgrad_ws_bytes bounds
+ * that need.  Calls that overlap on one GPU share that array and race. */
+int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T,
+                                    int64_t D, int64_t E, int64_t K, int dtype, void* dw_DE, void* stream);
+
 /* Backward of router.py:49-51 and the sigmoid of :45 when Router.forward is
  * used on its own: dL/dweights -> dlogit_TK. */
 int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const float* score_TK, int64_t T,
