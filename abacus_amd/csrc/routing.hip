@@ -290,20 +290,28 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
 }
 
 // ---------------------------------------------------------------------------
-// K3: permutation + gather.  Wave 0 ranks the block's 16 tokens inside each
+// K3: permutation + gather.  Block (b, y) takes token block b (16 tokens) and
+// column chunk y of their rows.  Wave 0 ranks the 16 tokens inside each
 // expert with one ballot per expert (ascending token order), giving every
-// (token, slot) its dispatched row; then the whole block copies each token
-// row once from HBM and writes it to its K destinations.
+// (token, slot) its dispatched row (the y == 0 block writes pos and perm);
+// then the block copies the chunk of each token row once and writes it to
+// the token's K destinations, kPermuteBatch vectors per thread loaded before
+// any is stored.  Splitting the columns over gridDim.y keeps enough blocks
+// (and loads) in flight when there are few tokens.
 // ---------------------------------------------------------------------------
+constexpr int kPermuteBatch = 8;
+
 template <typename T>
 __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict__ x, const int32_t* __restrict__ idx,
                                                              const int32_t* __restrict__ base, int T_, int D, int E,
                                                              int K, int32_t* __restrict__ pos,
                                                              int32_t* __restrict__ perm, T* __restrict__ xp) {
   constexpr int VEC = VecTraits<T>::kN;
+  constexpr int U = kPermuteBatch;
   __shared__ int s_pos[kRouteTB][kMaxK];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * kRouteTB;
+  const bool writer = blockIdx.y == 0;
   if (tid < 64) {
     const int lane = tid;
     const int t = t0 + lane;
@@ -322,20 +330,36 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
       if (slot >= 0) {
         const int rank = __popcll(m & lt);
         const int p = base[(int64_t)blockIdx.x * E + e] + rank;
-        pos[(int64_t)t * K + slot] = p;
-        perm[p] = t;
+        if (writer) {
+          pos[(int64_t)t * K + slot] = p;
+          perm[p] = t;
+        }
         s_pos[lane][slot] = p;
       }
     }
   }
   __syncthreads();
   const int nvec = D / VEC;
+  const int per = (nvec + gridDim.y - 1) / gridDim.y;  // columns of this chunk
+  const int c0 = blockIdx.y * per;
+  const int ncol = max(0, min(nvec, c0 + per) - c0);
   const int ntok = min(kRouteTB, T_ - t0);
-  for (int tok = 0; tok < ntok; ++tok) {
-    const T* src = x + (int64_t)(t0 + tok) * D;
-    for (int c = tid; c < nvec; c += 256) {
-      const Vec16 v = ld16(src + c * VEC);
-      for (int k = 0; k < K; ++k) st16(xp + (int64_t)s_pos[tok][k] * D + c * VEC, v);
+  const int total = ntok * ncol;
+  for (int i0 = 0; i0 < total; i0 += 256 * U) {
+    Vec16 v[U];
+    int tok[U], col[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * 256 + tid;
+      tok[u] = i / ncol;
+      col[u] = c0 + i % ncol;
+      if (i < total) v[u] = ld16(x + (int64_t)(t0 + tok[u]) * D + (int64_t)col[u] * VEC);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * 256 + tid;
+      if (i < total)
+        for (int k = 0; k < K; ++k) st16(xp + (int64_t)s_pos[tok[u]][k] * D + (int64_t)col[u] * VEC, v[u]);
     }
   }
 }
@@ -1060,11 +1084,15 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
   if (nb == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
+  // column chunks of at least 64 vectors, enough of them for ~1024 blocks
+  const int64_t nvec = D / vec_elems(dtype);
+  const unsigned ysplit = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nvec / 64, (1024 + nb - 1) / nb));
+  const dim3 grid((unsigned)nb, ysplit);
   if (dtype == kBF16)
-    hipLaunchKernelGGL(permute_gather_kernel<uint16_t>, dim3(nb), dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
+    hipLaunchKernelGGL(permute_gather_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
                        base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD);
   else
-    hipLaunchKernelGGL(permute_gather_kernel<float>, dim3(nb), dim3(256), 0, s, (const float*)x_TD, idx_TK, base,
+    hipLaunchKernelGGL(permute_gather_kernel<float>, grid, dim3(256), 0, s, (const float*)x_TD, idx_TK, base,
                        (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD);
   ABACUS_CHECK_LAUNCH("permute_gather");
   return 0;
