@@ -1,10 +1,13 @@
 """Benchmark: MoE-layer forward + backward tokens/s on one MI355X.
 
 Workload: the Mixtral-shaped layer (T = 2 x 2048 tokens, d_model 4096, 8 experts,
-top-2 sigmoid router, SwiGLU hidden 14336, bf16 with fp32 accumulation), synthetic
-inputs and N(0, 0.02^2) weights drawn on the GPU.  One step = forward of the layer,
-MSE loss against an N(0, 1) target, backward to x and every parameter (train mode,
-so the router's bias step runs too).
+top-2 sigmoid router, SwiGLU hidden 14336, bf16 with fp32 accumulation), built by
+the workload recipe on the host (seeded module init, N(0, 0.02^2) weights, N(0, 1)
+activations and target), then moved to the GPU.  One step = forward of the layer,
+MSE loss against the target, backward to x and every parameter (train mode, so the
+router's bias step runs too; the bias is reset before every step, so every step
+routes the same way).  Forward-only workloads (the small skewed batches) run the
+forward under no_grad.
 
 Prints one JSON line with the throughput, the roofline position of the dominant
 kernel (device time from HIP events recorded on the launch stream around every
@@ -75,6 +78,16 @@ def hbm_bytes(wl, name):
     return None
 
 
+def weight_stream_bytes(wl, e_touched):
+    """Bytes per launch of the forward expert products at decode-sized batches (inference: no G, U
+    saved): the touched experts' weights, the routed rows in, the product rows out."""
+    s, R, D, M = wl.elem_bytes(), wl.rows, wl.dim, wl.hidden
+    return {
+        "abacus_moe_gateup_fwd": s * (2 * e_touched * D * M + R * D + R * M),
+        "abacus_moe_down_fwd": s * (e_touched * M * D + R * M + R * D),
+    }
+
+
 TRAFFIC_FILE = "profiles/hbm_traffic_mixtral_bf16_fwd_bwd.md"
 
 
@@ -92,31 +105,27 @@ def measured_traffic(name):
     return None
 
 
-def cpu_baseline(wl, target_seconds):
-    """Oracle (the reference algorithm restated) on host cores, bounded token sample."""
+def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
+    """Oracle (the reference algorithm restated) on host cores, on the same layer's weights and
+    the first tokens of the same inputs (a bounded sample)."""
     from oracle import moe_oracle as oracle
-    from abacus_amd import workloads as W
 
     cores = min(len(os.sched_getaffinity(0)), 16)
     torch.set_num_threads(cores)
-    gen = torch.Generator().manual_seed(wl.seed)
-    D, E, M, K = wl.dim, wl.n_experts, wl.hidden, wl.top_k
-    dt = wl.dtype
-    # weights drawn on the GPU (fast) and copied once; same shapes and distribution
-    g = torch.Generator(device="cuda").manual_seed(wl.seed)
-    def draw(*shape):
-        return torch.randn(*shape, device="cuda", generator=g).mul_(0.02).to(dt).cpu()
-    w_DE, wg, wu, wd = draw(D, E), draw(E, D, M), draw(E, D, M), draw(E, M, D)
-    bias = torch.zeros(E, dtype=dt)
+    D, K = wl.dim, wl.top_k
+    w_DE, wg, wu, wd = (state[k] for k in ("router.w_DE", "w_gate_EDM", "w_up_EDM", "w_down_EMD"))
+    bias = state["router.expert_bias_E"]
+    xs, ts = x_cpu.reshape(-1, D), target_cpu.reshape(-1, D)
 
     def run(tokens):
-        x = torch.randn(tokens, D, generator=gen).to(dt).requires_grad_()
-        target = torch.randn(tokens, D, generator=gen).to(dt)
-        params = [t.clone().requires_grad_() for t in (w_DE, wg, wu, wd)]
+        x = xs[:tokens].clone().requires_grad_(wl.backward)
+        params = [t.clone().requires_grad_(wl.backward) for t in (w_DE, wg, wu, wd)]
         t0 = time.perf_counter()
-        out, _ = oracle.moe_forward(x, params[0], bias, params[1], params[2], params[3], K, 1.0)
-        loss = (out.float() - target.float()).pow(2).mean()
-        loss.backward()
+        with torch.set_grad_enabled(wl.backward):
+            out, _ = oracle.moe_forward(x, params[0], bias, params[1], params[2], params[3], K, 1.0)
+            if wl.backward:
+                loss = (out.float() - ts[:tokens].float()).pow(2).mean()
+                loss.backward()
         return time.perf_counter() - t0
 
     tokens = 16
@@ -142,10 +151,11 @@ def cpu_baseline(wl, target_seconds):
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{wl.name} layer shape (D={D}, E={E}, K={K}, M={M}, {str(dt).replace('torch.', '')}) on "
-                   f"{tokens} of {wl.tokens} tokens, fwd+bwd of the oracle's restatement of router.py:40-70 + "
-                   f"moe.py:60-86, median of {len(times)} runs ({med:.2f} s each); torch CPU threads={cores}, "
-                   f"os.cpu_count={os.cpu_count()}, cpu='{cpu_model}'"),
+        "sample": (f"{wl.name} layer (D={D}, E={wl.n_experts}, K={K}, M={wl.hidden}, "
+                   f"{str(wl.dtype).replace('torch.', '')}, the benchmark's own weights) on the first {tokens} of its "
+                   f"{wl.tokens} tokens, {'fwd+bwd' if wl.backward else 'fwd'} of the oracle's restatement of "
+                   f"router.py:40-70 + moe.py:60-86, median of {len(times)} runs ({med:.2f} s each); torch CPU "
+                   f"threads={cores}, os.cpu_count={os.cpu_count()}, cpu='{cpu_model}'"),
     }
 
 
@@ -235,14 +245,19 @@ def main():
     wl = W.ALL[args.workload]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    moe, x, target = W.build_on_device(wl, dev)
+    moe, x_cpu, target_cpu = W.build(wl)  # the workload recipe, on the host
+    state = {k: v.detach().clone() for k, v in moe.state_dict().items()} if not args.no_cpu_baseline else None
+    moe = moe.to(dev)
+    x, target = x_cpu.to(dev), target_cpu.to(dev)
     moe.train()
-    x = x.detach()
+    bias0 = moe.router.expert_bias_E.detach().clone()
 
     def step():
+        moe.router.expert_bias_E.copy_(bias0)  # every step routes as the first
         moe.zero_grad(set_to_none=True)
         xi = x.requires_grad_(wl.backward)
-        out = moe(xi)
+        with torch.set_grad_enabled(wl.backward):
+            out = moe(xi)
         if wl.backward:
             loss = torch.nn.functional.mse_loss(out, target)  # mean((y - target)^2)
             loss.backward()
@@ -289,7 +304,21 @@ def main():
     gemm_tf = wl.gemm_flops() / (gemm_ms / 1000.0) / 1e12 if gemm_ms else 0.0
     dominant = max(totals.items(), key=lambda kv: kv[1][0])[0]
     d_ms, d_n = totals[dominant]
-    if dominant in GEMM_FLOPS:
+    counts = moe.router.last_routing.counts_E
+    e_touched = int((counts > 0).sum()) if counts is not None else wl.n_experts
+    stream_bytes = weight_stream_bytes(wl, e_touched)
+    if not wl.backward and wl.rows <= 128 * wl.n_experts and dominant in stream_bytes:
+        # decode-sized batches: the expert products stream the touched experts' weights
+        b = stream_bytes[dominant]
+        achieved = b / (d_ms / d_n / 1000.0) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                    "algorithmic_per_launch": b, "experts_touched": e_touched}
+        for n, nb in stream_bytes.items():
+            if n in kernels:
+                gbs = nb / (kernels[n]["avg_us"] / 1e6) / 1e9
+                kernels[n].update({"gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+    elif dominant in GEMM_FLOPS:
         achieved = GEMM_FLOPS[dominant] * R * D * M / (d_ms / d_n / 1000.0) / 1e12
         traffic = measured_traffic(dominant) if wl.name == "mixtral_bf16" else None
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 1), "peak": peak_mfma,
@@ -315,8 +344,10 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16" if wl.dtype == torch.bfloat16 else "fp32",
-        "data": "synthetic (N(0,1) activations and target, N(0,0.02^2) weights, drawn on the GPU)",
-        "config": {"workload": f"{wl.name}: MoE layer fwd+bwd, T={wl.tokens} (batch {wl.batch} x seq {wl.seq}), "
+        "data": (f"synthetic, the workload recipe: seed {wl.seed}, module init on the host, N(0,0.02^2) weights, "
+                 "N(0,1) activations and target" + (", Zipf(1.2) selection bias" if wl.zipf_bias else "")),
+        "config": {"workload": f"{wl.name}: MoE layer {'fwd+bwd' if wl.backward else 'fwd'}, T={wl.tokens} "
+                               f"(batch {wl.batch} x seq {wl.seq}), "
                                f"D={wl.dim}, E={wl.n_experts}, K={wl.top_k}, M={wl.hidden}",
                    "tokens": wl.tokens, "d_model": wl.dim, "n_experts": wl.n_experts, "top_k": wl.top_k,
                    "hidden": wl.hidden},
@@ -326,7 +357,7 @@ def main():
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(wl, state, x_cpu, target_cpu, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 
 
