@@ -128,12 +128,15 @@ def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
                 loss.backward()
         return time.perf_counter() - t0
 
-    tokens = 16
-    el = run(tokens)  # warm-up + calibration
-    while el < target_seconds / 4 and tokens < wl.tokens:
-        tokens = min(wl.tokens, tokens * 2)
-        el = run(tokens)
-    times = [el]
+    # Sample size: a step of the reference algorithm costs a fixed part (its per-expert weight
+    # slices and their gradients) plus a part per token; both are fitted from 16 and 64 tokens,
+    # and the sample is the most tokens whose predicted step fits a third of the time budget.
+    run(16)  # warm-up
+    t16, t64 = run(16), run(min(64, wl.tokens))
+    per_token = max((t64 - t16) / 48.0, 1e-7)
+    fixed = max(t16 - 16 * per_token, 0.0)
+    tokens = int(min(wl.tokens, max(16, (target_seconds / 3 - fixed) / per_token)))
+    times = [run(tokens)]
     while sum(times) < target_seconds and len(times) < 5:
         times.append(run(tokens))
     med = statistics.median(times)
@@ -154,8 +157,9 @@ def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
         "sample": (f"{wl.name} layer (D={D}, E={wl.n_experts}, K={K}, M={wl.hidden}, "
                    f"{str(wl.dtype).replace('torch.', '')}, the benchmark's own weights) on the first {tokens} of its "
                    f"{wl.tokens} tokens, {'fwd+bwd' if wl.backward else 'fwd'} of the oracle's restatement of "
-                   f"router.py:40-70 + moe.py:60-86, median of {len(times)} runs ({med:.2f} s each); torch CPU "
-                   f"threads={cores}, os.cpu_count={os.cpu_count()}, cpu='{cpu_model}'"),
+                   f"router.py:40-70 + moe.py:60-86, median of {len(times)} runs ({med:.2f} s each; fitted fixed "
+                   f"cost per step {fixed:.2f} s + {per_token * 1e6:.1f} us per token); torch CPU threads={cores}, "
+                   f"os.cpu_count={os.cpu_count()}, cpu='{cpu_model}'"),
     }
 
 
