@@ -1,7 +1,9 @@
 """ctypes binding of libabacus_moe.so (declarations in include/abacus_moe.h).
 
-The library is the only compute path for device tensors: if it is missing the
-first call raises, there is no fallback.
+The HIP library is the only compute path for GPU tensors: if it is missing the
+first call raises, there is no fallback.  CPU tensors go to libabacus_moe_host.so,
+a host C++ build of the same entry points (abacus_amd/csrc/host/moe_host.cpp): a
+call whose stream argument is stream_of(a CPU device) runs there.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import threading
 import torch
 
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "libabacus_moe.so"
+HOST_LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "libabacus_moe_host.so"
 
 F32 = 0
 BF16 = 1
@@ -70,8 +73,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_adamw_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _D, _D, _D, _D, _D, _I, _P]),
 }
 
+# Entry points of the HIP library that the host library also provides: the MoE layer, the router and
+# the load-balancing loss (the decoder's RMSNorm, attention, cross-entropy and AdamW entry points are
+# GPU-only; on the CPU those modules use torch).
+HOST_SYMBOLS = [n for n in SIGNATURES if n.startswith("abacus_moe_") or n.startswith("abacus_router_")]
+
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_host_lib: ctypes.CDLL | None = None
 
 
 def load() -> ctypes.CDLL:
@@ -93,6 +102,35 @@ def load() -> ctypes.CDLL:
                 fn.argtypes = args
             _lib = lib
     return _lib
+
+
+def load_host() -> ctypes.CDLL:
+    """Load libabacus_moe_host.so (the entry points for CPU tensors) once."""
+    global _host_lib
+    if _host_lib is not None:
+        return _host_lib
+    with _lock:
+        if _host_lib is None:
+            if not HOST_LIB_PATH.exists():
+                raise RuntimeError(f"{HOST_LIB_PATH} is not built: run `python -m abacus_amd.build`")
+            lib = ctypes.CDLL(str(HOST_LIB_PATH))
+            for name in HOST_SYMBOLS:
+                res, args = SIGNATURES[name]
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _host_lib = lib
+    return _host_lib
+
+
+class _HostStream:
+    """The stream argument of a call on CPU tensors: routes the call to the host library."""
+
+    def __repr__(self) -> str:
+        return "<host>"
+
+
+HOST = _HostStream()
 
 
 class KernelTimer:
@@ -128,7 +166,17 @@ _timer: KernelTimer | None = None
 
 
 def call(name: str, *args) -> None:
-    """Call an entry point that returns a status code; raise on failure."""
+    """Call an entry point that returns a status code; raise on failure.
+
+    The last argument is the stream: stream_of(device) of the tensors' device.  HOST (a CPU
+    device's) runs the host library's entry point instead of the HIP one."""
+    if args and args[-1] is HOST:
+        lib = load_host()
+        rc = getattr(lib, name)(*args[:-1], None)
+        if rc != 0:
+            msg = lib.abacus_moe_last_error().decode(errors="replace")
+            raise RuntimeError(f"{name} failed ({rc}): {msg}")
+        return
     lib = load()
     timer = _timer
     if timer is not None:
@@ -144,8 +192,10 @@ def call(name: str, *args) -> None:
         timer.events.append((name, start, end))
 
 
-def query(name: str, *args) -> int:
-    return int(getattr(load(), name)(*args))
+def query(name: str, *args, device: torch.device | None = None) -> int:
+    """A sizing query, answered by the library that will run on `device` (the HIP one by default)."""
+    lib = load_host() if device is not None and device.type == "cpu" else load()
+    return int(getattr(lib, name)(*args))
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -173,5 +223,8 @@ def tile_ctr(device: torch.device) -> torch.Tensor:
     return torch.empty(TILE_CTR_INTS, dtype=torch.int32, device=device)
 
 
-def stream_of(device: torch.device) -> int:
+def stream_of(device: torch.device):
+    """The stream argument for a call on `device`'s tensors: torch's current HIP stream, or HOST."""
+    if device.type == "cpu":
+        return HOST
     return torch.cuda.current_stream(device).cuda_stream

@@ -1,7 +1,10 @@
-"""Build recipe for libabacus_moe.so (the MI355X / gfx950 MoE kernel library).
+"""Build recipe for libabacus_moe.so (the MI355X / gfx950 MoE kernel library) and
+libabacus_moe_host.so (the same C ABI built for CPU tensors).
 
 Compiles every ``abacus_amd/csrc/*.hip`` translation unit with hipcc for
-gfx950 and links them into ``abacus_amd/lib/libabacus_moe.so`` in-tree.
+gfx950 and links them into ``abacus_amd/lib/libabacus_moe.so`` in-tree, and
+``abacus_amd/csrc/host/moe_host.cpp`` with g++ (OpenMP) into
+``abacus_amd/lib/libabacus_moe_host.so``.
 Run ``python -m abacus_amd.build`` (or ``__graft_entry__.build()``).
 """
 
@@ -19,6 +22,9 @@ INCLUDE = PKG.parent / "include"
 CSRC = PKG / "csrc"
 LIB_DIR = PKG / "lib"
 LIB_NAME = "libabacus_moe.so"
+HOST_LIB_NAME = "libabacus_moe_host.so"
+# portable x86-64 code (no -march=native): the library is built here and runs on other hosts
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-fopenmp", "-shared", "-Wall", "-Wno-unused-parameter"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (see DESIGN notes on
@@ -54,8 +60,26 @@ def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
 
 
+def build_host(verbose: bool = True) -> pathlib.Path:
+    """Compile the host C++ build of the C ABI (CPU tensors)."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("g++ not found; it builds libabacus_moe_host.so")
+    LIB_DIR.mkdir(exist_ok=True)
+    out = LIB_DIR / HOST_LIB_NAME
+    tmp = LIB_DIR / (HOST_LIB_NAME + ".tmp")
+    cmd = [cxx, *HOST_FLAGS, f"-I{INCLUDE}", str(CSRC / "host" / "moe_host.cpp"), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for moe_host.cpp:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}", file=sys.stderr)
+    return out
+
+
 def build(verbose: bool = True) -> pathlib.Path:
-    """Compile all HIP sources for gfx950 and link the shared library."""
+    """Compile all HIP sources for gfx950 and link the shared library, then the host library."""
     obj_dir = PKG / "_build"
     obj_dir.mkdir(exist_ok=True)
     LIB_DIR.mkdir(exist_ok=True)
@@ -75,6 +99,7 @@ def build(verbose: bool = True) -> pathlib.Path:
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}", file=sys.stderr)
+    build_host(verbose)
     return out
 
 

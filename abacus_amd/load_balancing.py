@@ -23,7 +23,8 @@ class _LoadBalancingLoss(torch.autograd.Function):
         T, E = probs_TE.shape
         K = slots_TK.shape[1]
         dev, dt = probs_TE.device, _lib.dtype_code(probs_TE.dtype)
-        ws = torch.empty(_lib.query("abacus_moe_load_balancing_ws_bytes", T, E), dtype=torch.uint8, device=dev)
+        ws = torch.empty(_lib.query("abacus_moe_load_balancing_ws_bytes", T, E, device=dev), dtype=torch.uint8,
+                         device=dev)
         f_E = torch.empty(E, dtype=torch.float32, device=dev)
         loss32 = torch.empty((), dtype=torch.float32, device=dev)
         loss = torch.empty((), dtype=probs_TE.dtype, device=dev)

@@ -46,10 +46,10 @@ class Routing:
 
 
 def _check_device(x: torch.Tensor, what: str) -> None:
-    if x.device.type != "cuda":
+    """GPU tensors run on the HIP library, CPU tensors on its host build; nothing else is accepted."""
+    if x.device.type not in ("cuda", "cpu"):
         raise RuntimeError(
-            f"abacus_amd {what} runs on ROCm (HIP) devices only; got a tensor on {x.device}. "
-            "Move the module and its inputs to a GPU."
+            f"abacus_amd {what} runs on ROCm (HIP) GPUs and on the CPU; got a tensor on {x.device}."
         )
 
 
@@ -71,8 +71,8 @@ def _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale):
     indices = torch.empty(T, top_k, dtype=torch.int64, device=dev)
     idx32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
     score = torch.empty(T, top_k, dtype=torch.float32, device=dev)
-    hist = torch.empty(query("abacus_moe_hist_len", T, E), dtype=torch.int32, device=dev)
-    wt = torch.empty(query("abacus_moe_router_ws_bytes", D, E, dt), dtype=torch.uint8, device=dev)
+    hist = torch.empty(query("abacus_moe_hist_len", T, E, device=dev), dtype=torch.int32, device=dev)
+    wt = torch.empty(query("abacus_moe_router_ws_bytes", D, E, dt, device=dev), dtype=torch.uint8, device=dev)
     call(
         "abacus_moe_router_fwd", ptr(x_TD), ptr(w_DE), ptr(bias_E), T, D, E, top_k, float(route_scale), dt,
         ptr(logits), ptr(weights), ptr(indices), ptr(idx32), ptr(score), ptr(hist), ptr(wt), _lib.stream_of(dev),
@@ -97,7 +97,7 @@ def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos
         )
     if ctx_needs_w:
         dw = torch.empty_like(w_DE)
-        nbytes = query("abacus_moe_router_wgrad_ws_bytes", T, D, E)
+        nbytes = query("abacus_moe_router_wgrad_ws_bytes", T, D, E, device=dev)
         partial = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
         call("abacus_moe_router_wgrad", ptr(x_TD), ptr(dlogit), ptr(idx32), T, D, E, K, dt, ptr(partial), ptr(dw), s)
     return dx, dw
@@ -165,7 +165,7 @@ class _MoEFunction(torch.autograd.Function):
             ptr(gate), ptr(up), ptr(h), s,
         )
         y = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
-        ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, E, dt)
+        ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, E, dt, device=dev)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
         call("abacus_moe_down_fwd", ptr(h), ptr(w_down), ptr(offsets), R, M, D, E, dt, ptr(y), ptr(ws), ws_bytes, s)
         out = torch.empty(T, D, dtype=x_TD.dtype, device=dev)

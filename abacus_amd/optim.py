@@ -2,9 +2,10 @@
 
 Same constructor, validation, state layout ({"step", "exp_avg", "exp_avg_sq"}
 per parameter, keyed by id, moments in the parameter's dtype) and per-element
-arithmetic as the reference's AdamW; ``step()`` updates every parameter with a
+arithmetic as the reference's AdamW; ``step()`` updates every GPU parameter with a
 gradient in one pass per tensor group (``abacus_adamw_step``: one HIP launch
-per 48 tensors) instead of eight tensor ops per parameter.  ZeRO's owned
+per 48 tensors) instead of eight tensor ops per parameter.  CPU parameters take
+the reference's eight torch ops.  ZeRO's owned
 slices and gradient shards (``owned``, ``grad_shards``) belong to the
 reference's multi-GPU data parallelism and are not taken here.
 """
@@ -63,8 +64,6 @@ class AdamW:
                 continue
             if grad.is_sparse:
                 raise RuntimeError("AdamW does not support sparse gradients")
-            if not param.is_cuda:
-                raise RuntimeError(f"abacus_amd AdamW updates GPU parameters (got one on {param.device})")
             state = self.state.get(id(param))
             if state is None:
                 state = {
@@ -74,6 +73,9 @@ class AdamW:
                 }
                 self.state[id(param)] = state
             state["step"] += 1
+            if not param.is_cuda:
+                self._step_cpu(param, grad, state)
+                continue
             if not grad.is_contiguous() or grad.dtype != param.dtype:
                 grad = grad.contiguous().to(param.dtype)
             groups.setdefault((param.dtype, param.device), []).append(
@@ -85,6 +87,18 @@ class AdamW:
             steps = (ctypes.c_int64 * n)(*[it[4] for it in items])
             _lib.call("abacus_adamw_step", *ptrs, numels, steps, n, self.lr, self.beta1, self.beta2, self.eps,
                       self.weight_decay, _lib.dtype_code(dtype), _lib.stream_of(device))
+
+
+    def _step_cpu(self, weight: torch.Tensor, grad: torch.Tensor, state: dict) -> None:
+        """One parameter's update as the reference's op sequence (optimizers/adamw.py:107-119)."""
+        exp_avg, exp_avg_sq = state["exp_avg"], state["exp_avg_sq"]
+        if self.weight_decay != 0:
+            weight.mul_(1 - self.lr * self.weight_decay)
+        exp_avg.lerp_(grad, 1 - self.beta1)
+        exp_avg_sq.mul_(self.beta2).addcmul_(grad, grad, value=1 - self.beta2)
+        step_size = self.lr / (1 - self.beta1 ** state["step"])
+        denom = exp_avg_sq.sqrt().div_((1 - self.beta2 ** state["step"]) ** 0.5).add_(self.eps)
+        weight.addcdiv_(exp_avg, denom, value=-step_size)
 
 
 class WSD:

@@ -7,6 +7,7 @@ import pathlib
 import re
 
 import pytest
+import torch
 
 from abacus_amd import _lib
 
@@ -40,6 +41,18 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_lib.LIB_PATH))
     for name in _declarations():
         assert hasattr(lib, name), name
+
+
+def test_host_library_exports_its_entry_points():
+    """libabacus_moe_host.so (CPU tensors) exports every MoE-layer, router and load-balancing entry
+    point of the header, with the same ABI version."""
+    lib = ctypes.CDLL(str(_lib.HOST_LIB_PATH))
+    decls = _declarations()
+    assert len(_lib.HOST_SYMBOLS) >= 25
+    for name in _lib.HOST_SYMBOLS:
+        assert name in decls and hasattr(lib, name), name
+    assert _lib.load_host().abacus_moe_abi_version() == 2
+    assert _lib.query("abacus_moe_hist_len", 4096, 8, device=torch.device("cpu")) == (4096 // 16) * 8
 
 
 def test_abi_version_and_queries():

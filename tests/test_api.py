@@ -76,13 +76,13 @@ def test_bf16_cast_moves_bias_buffer():
     assert moe.w_gate_EDM.dtype == torch.bfloat16
 
 
-def test_cpu_tensors_fail_loudly():
-    """There is no CPU implementation behind the module: a CPU call raises, it never falls back."""
-    moe = MoE(8, 4, 2)
+def test_other_devices_fail_loudly():
+    """GPU tensors run on the HIP library and CPU tensors on its host build; any other device raises."""
+    moe = MoE(8, 4, 2).to("meta")
     with pytest.raises(RuntimeError, match="ROCm"):
-        moe(torch.randn(1, 3, 8))
+        moe(torch.randn(1, 3, 8, device="meta"))
     with pytest.raises(RuntimeError, match="ROCm"):
-        Router(8, 4, 2)(torch.randn(1, 3, 8))
+        Router(8, 4, 2).to("meta")(torch.randn(1, 3, 8, device="meta"))
 
 
 def test_dense_mlp_matches_linear_layers():
@@ -124,4 +124,4 @@ def test_load_balancing_empty_and_cpu():
     z = load_balancing_loss(torch.zeros(0, 5, dtype=torch.bfloat16), torch.zeros(0, 2, dtype=torch.long))
     assert z.shape == () and z.dtype == torch.bfloat16 and float(z) == 0.0
     with pytest.raises(RuntimeError, match="ROCm"):
-        load_balancing_loss(torch.rand(4, 3), torch.zeros(4, 1, dtype=torch.long))
+        load_balancing_loss(torch.rand(4, 3, device="meta"), torch.zeros(4, 1, dtype=torch.long, device="meta"))

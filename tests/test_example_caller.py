@@ -4,8 +4,9 @@ The example imports (examples/train_gpt_moe.py:12-16) resolve to this package, a
 single-process flow -- documents from a {"tokens": [1-D LongTensor], "vocab_size": int} file
 (:26-33), documents under 2 tokens dropped and --limit applied (:36-49), batches of 4 padded
 with -100 (:52-65), seed 0, TransformerMoe(DIM, N_HEADS, HEAD_DIM, N_BLOCKS, vocab, E=4, K=1)
-and Trainer(model, total_steps) stepping over the batches (:91-134) -- trains on one GPU: the
-loss is finite and falls, and every router's selection bias moves (router.py:52-53).  The data
+and Trainer(model, total_steps) stepping over the batches (:91-134) -- trains on one GPU, and on
+the CPU (the MoE layers on the host build of the library): the loss is finite and falls, and
+every router's selection bias moves (router.py:52-53).  The data
 file is synthetic (Zipf-distributed token ids), written by the test; the reference's data
 comes from a network-bound prep script.
 """
@@ -13,6 +14,7 @@ comes from a network-bound prep script.
 from __future__ import annotations
 
 import os
+import sys
 
 import pytest
 import torch
@@ -69,8 +71,7 @@ def _run_example(path, limit):
     return losses, moved, total_steps
 
 
-@pytest.mark.gpu
-def test_example_trains_on_one_gpu(tmp_path):
+def _check_training(tmp_path):
     path = tmp_path / "docs.pt"
     _write_documents(path)
     losses, moved, total_steps = _run_example(path, limit=40)
@@ -79,6 +80,18 @@ def test_example_trains_on_one_gpu(tmp_path):
     assert all(torch.isfinite(torch.tensor(losses)))
     assert sum(losses[-2:]) < sum(losses[:2])
     assert all(moved)
+
+
+@pytest.mark.gpu
+def test_example_trains_on_one_gpu(tmp_path):
+    _check_training(tmp_path)
+
+
+def test_example_trains_on_cpu(tmp_path, monkeypatch):
+    import abacus_amd.train as train
+    monkeypatch.setattr(train, "get_device", lambda: torch.device("cpu"))
+    monkeypatch.setattr(sys.modules[__name__], "get_device", lambda: torch.device("cpu"))
+    _check_training(tmp_path)
 
 
 def test_process_group_helpers_single_process(monkeypatch):
