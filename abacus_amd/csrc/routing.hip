@@ -15,14 +15,15 @@
 
 #include <climits>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
 namespace abacus {
 
 constexpr int kRouteTB = 16;   // tokens per router / permute block (one MFMA row tile)
-constexpr int kMaxE = 64;      // experts handled by the fused router
-constexpr int kMaxK = 8;       // slots per token handled by the fused kernels
+constexpr int kMaxE = 256;     // experts handled by the fused router
+constexpr int kMaxK = 16;      // slots per token handled by the fused kernels
 constexpr int64_t kScanLdsBytes = 48 * 1024;  // route_scan stages histograms up to this size in LDS
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -65,11 +66,28 @@ __global__ void transpose_router_weight_kernel(const T* __restrict__ w, T* __res
   }
 }
 
+// Selection key of expert e with selection value v: larger keys rank first
+// in torch.topk's order -- NaN above every number, then larger values, then
+// the lower expert index among equals (-0.0 and +0.0 are equal).  The high
+// word maps v to an order-preserving unsigned integer, the low word is ~e.
+// Every real key exceeds 0, the key of a retired or absent expert.
+__device__ inline uint64_t selection_key(float v, int e) {
+  uint32_t hi;
+  if (v != v) {
+    hi = 0xFFFFFFFFu;
+  } else {
+    const uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+    hi = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)e;
+}
+
 // ---------------------------------------------------------------------------
 // K1: fused router.  One block = 16 tokens x all experts; the 4 waves split
 // the D reduction (k-blocks interleaved), partials are summed in LDS in a
-// fixed order, then one thread per token runs the sigmoid / bias / top-k /
-// renormalise epilogue and bumps the block's expert histogram.
+// fixed order, the sigmoid and bias are applied per (token, expert), then one
+// wave per token runs the top-k / renormalise epilogue and bumps the block's
+// expert histogram.
 // ---------------------------------------------------------------------------
 template <typename T, int NF>
 __global__ __launch_bounds__(256) void router_fwd_kernel(
@@ -82,13 +100,13 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   __shared__ float red[4][kRouteTB][EP];
   __shared__ float s_sc[kRouteTB][EP];
   __shared__ float s_sel[kRouteTB][EP];
-  __shared__ int s_cnt[kMaxE];
+  __shared__ int s_cnt[EP];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int t0 = blockIdx.x * kRouteTB;
-  if (tid < kMaxE) s_cnt[tid] = 0;
+  for (int i = tid; i < EP; i += 256) s_cnt[i] = 0;
 
   f32x4_t acc[NF];
 #pragma unroll
@@ -101,7 +119,7 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   const bool vec_ok = (D % VEC) == 0;  // rows are 16-byte aligned only then
   // U k-blocks per batch, all their loads in flight before their MFMAs: one
   // k-block at a time left the pass waiting out a memory latency per k-block.
-  constexpr int U = NF <= 2 ? 8 : 4;
+  constexpr int U = NF <= 2 ? 8 : (NF <= 4 ? 4 : (NF <= 8 ? 2 : 1));
   int kb0 = wave * KB;
   if (vec_ok) {
     for (; kb0 + (U - 1) * 4 * KB < D; kb0 += U * 4 * KB) {
@@ -167,53 +185,56 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   }
   __syncthreads();
 
-  if (tid < kRouteTB && t0 + tid < T_) {
-    const int tok = tid;
+  // Top-K, one wave per token (4 tokens per wave): lane l holds experts l,
+  // l + 64, ... as selection keys; each of the K rounds takes the wave maximum
+  // key and retires that expert.
+  constexpr int CPL = EP <= 64 ? 1 : EP / 64;  // experts per lane
+  for (int tok = wave; tok < kRouteTB; tok += 4) {
     const int t = t0 + tok;
-    uint64_t taken = 0;
-    float picked[kMaxK];
-    int picked_e[kMaxK];
-    float sum = 0.f;
+    if (t >= T_) break;  // the same for the whole wave
+    uint64_t key[CPL];
 #pragma unroll
-    for (int k = 0; k < kMaxK; ++k) {
-      if (k < K) {
-        int best_e = -1;
-        float best = 0.f;
-        bool best_nan = false;
-        for (int e = 0; e < E; ++e) {
-          if ((taken >> e) & 1ull) continue;
-          const float v = s_sel[tok][e];
-          const bool v_nan = v != v;
-          // torch.topk orders NaN above every number; ties keep the lower index.
-          const bool better = (best_e < 0) || (v_nan && !best_nan) || (!v_nan && !best_nan && v > best);
-          if (better) {
-            best_e = e;
-            best = v;
-            best_nan = v_nan;
-          }
-        }
-        taken |= 1ull << best_e;
-        picked_e[k] = best_e;
-        picked[k] = s_sc[tok][best_e];
-        sum += picked[k];
-        atomicAdd(&s_cnt[best_e], 1);
-      }
+    for (int c = 0; c < CPL; ++c) {
+      const int e = lane + 64 * c;
+      key[c] = e < E ? selection_key(s_sel[tok][e], e) : 0ull;
     }
-    const float denom = round_to<T>(sum);
+    float sum = 0.f, my_s = 0.f;
+    int my_e = 0;
+    for (int k = 0; k < K; ++k) {
+      uint64_t best = key[0];
 #pragma unroll
-    for (int k = 0; k < kMaxK; ++k) {
-      if (k < K) {
-        const float w = round_to<T>(round_to<T>(picked[k] / denom) * route_scale);
-        const int64_t o = (int64_t)t * K + k;
-        weights[o] = from_f32<T>(w);
-        indices[o] = picked_e[k];
-        idx32[o] = picked_e[k];
-        score[o] = picked[k];
+      for (int c = 1; c < CPL; ++c) best = key[c] > best ? key[c] : best;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)best, off, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        best = o > best ? o : best;
       }
+      const int be = (int)(~(uint32_t)best);
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+        if (lane + 64 * c == be) key[c] = 0ull;
+      const float sc = s_sc[tok][be];
+      sum += sc;  // pick order
+      if (lane == k) {
+        my_s = sc;
+        my_e = be;
+      }
+      if (lane == 0) atomicAdd(&s_cnt[be], 1);
+    }
+    if (lane < K) {
+      const float denom = round_to<T>(sum);
+      const float w = round_to<T>(round_to<T>(my_s / denom) * route_scale);
+      const int64_t o = (int64_t)t * K + lane;
+      weights[o] = from_f32<T>(w);
+      indices[o] = my_e;
+      idx32[o] = my_e;
+      score[o] = my_s;
     }
   }
   __syncthreads();
-  if (tid < E) hist[(int64_t)blockIdx.x * E + tid] = s_cnt[tid];
+  for (int e = tid; e < E; e += 256) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
 }
 
 // ---------------------------------------------------------------------------
@@ -238,19 +259,22 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
     __syncthreads();
   }
   auto hv = [&](int b, int e) -> int { return STAGED ? s_hist[b * E + e] : hist[(int64_t)b * E + e]; };
+  // 16 groups of 64 threads; group q sums blocks b0 .. b1-1, lane l experts l, l + 64, ...
   __shared__ int part[16][kMaxE];
   __shared__ int cnt[kMaxE];
   __shared__ int off[kMaxE + 1];
   const int tid = threadIdx.x;
-  const int e = tid & 63;
+  const int lane = tid & 63;
   const int q = tid >> 6;
   const int per = (nb + 15) / 16;
   const int b0 = q * per;
   const int b1 = min(nb, b0 + per);
-  int p = 0;
-  if (e < E)
-    for (int b = b0; b < b1; ++b) p += hv(b, e);
-  part[q][e] = p;
+  for (int e = lane; e < kMaxE; e += 64) {
+    int p = 0;
+    if (e < E)
+      for (int b = b0; b < b1; ++b) p += hv(b, e);
+    part[q][e] = p;
+  }
   __syncthreads();
   if (tid < kMaxE) {
     int c = 0;
@@ -279,7 +303,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
     }
   }
   if (tid == 0) offsets[E] = off[E];
-  if (e < E) {
+  for (int e = lane; e < E; e += 64) {
     int run = off[e];
     for (int i = 0; i < q; ++i) run += part[i][e];
     for (int b = b0; b < b1; ++b) {
@@ -291,9 +315,10 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
 
 // ---------------------------------------------------------------------------
 // K3: permutation + gather.  Block (b, y) takes token block b (16 tokens) and
-// column chunk y of their rows.  Wave 0 ranks the 16 tokens inside each
-// expert with one ballot per expert (ascending token order), giving every
-// (token, slot) its dispatched row (the y == 0 block writes pos and perm);
+// column chunk y of their rows.  Each of the block's (token, slot) pairs is
+// ranked inside its expert by counting the block's earlier tokens that picked
+// the same expert (a token's experts are distinct), which gives its dispatched
+// row (the y == 0 block writes pos and perm);
 // then the block copies the chunk of each token row once and writes it to
 // the token's K destinations, kPermuteBatch vectors per thread loaded before
 // any is stored.  Splitting the columns over gridDim.y keeps enough blocks
@@ -308,42 +333,36 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
                                                              int32_t* __restrict__ perm, T* __restrict__ xp) {
   constexpr int VEC = VecTraits<T>::kN;
   constexpr int U = kPermuteBatch;
+  static_assert(kRouteTB * kMaxK <= 256, "one thread per (token, slot) pair");
+  __shared__ int s_e[kRouteTB][kMaxK];
   __shared__ int s_pos[kRouteTB][kMaxK];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * kRouteTB;
   const bool writer = blockIdx.y == 0;
-  if (tid < 64) {
-    const int lane = tid;
-    const int t = t0 + lane;
-    const bool valid = lane < kRouteTB && t < T_;
-    int my_e[kMaxK];
-#pragma unroll
-    for (int k = 0; k < kMaxK; ++k) my_e[k] = (valid && k < K) ? idx[(int64_t)t * K + k] : -1;
-    const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
-    for (int e = 0; e < E; ++e) {
-      int slot = -1;
-#pragma unroll
-      for (int k = 0; k < kMaxK; ++k)
-        if (my_e[k] == e) slot = k;
-      const uint64_t m = __ballot(slot >= 0);
-      if (m == 0) continue;
-      if (slot >= 0) {
-        const int rank = __popcll(m & lt);
-        const int p = base[(int64_t)blockIdx.x * E + e] + rank;
-        if (writer) {
-          pos[(int64_t)t * K + slot] = p;
-          perm[p] = t;
-        }
-        s_pos[lane][slot] = p;
-      }
+  const int ntok = min(kRouteTB, T_ - t0);
+  if (tid < kRouteTB * K) {
+    const int tok = tid / K, k = tid % K;
+    s_e[tok][k] = tok < ntok ? idx[(int64_t)(t0 + tok) * K + k] : -1;
+  }
+  __syncthreads();
+  if (tid < ntok * K) {
+    const int tok = tid / K, k = tid % K;
+    const int e = s_e[tok][k];
+    int rank = 0;
+    for (int t2 = 0; t2 < tok; ++t2)
+      for (int k2 = 0; k2 < K; ++k2) rank += s_e[t2][k2] == e ? 1 : 0;
+    const int p = base[(int64_t)blockIdx.x * E + e] + rank;
+    if (writer) {
+      pos[(int64_t)(t0 + tok) * K + k] = p;
+      perm[p] = t0 + tok;
     }
+    s_pos[tok][k] = p;
   }
   __syncthreads();
   const int nvec = D / VEC;
   const int per = (nvec + gridDim.y - 1) / gridDim.y;  // columns of this chunk
   const int c0 = blockIdx.y * per;
   const int ncol = max(0, min(nvec, c0 + per) - c0);
-  const int ntok = min(kRouteTB, T_ - t0);
   const int total = ntok * ncol;
   for (int i0 = 0; i0 < total; i0 += 256 * U) {
     Vec16 v[U];
@@ -385,25 +404,25 @@ __device__ inline void sort_slots_by_expert(int K, int* e, int* p, float* w) {
 
 // Token t's K slots ordered by expert, read by every lane of a wave (the same
 // cache line): expert e, dispatched row p, coefficient w = coef(k).  A fixed
-// compare-exchange network keeps the arrays in registers; slots k >= K get
-// e = INT_MAX and sort last.  Exchanges only on a strictly greater expert, so
-// the order is the insertion sort's.
-template <typename Coef>
+// compare-exchange network over KB >= K slots keeps the arrays in registers;
+// slots k >= K get e = INT_MAX and sort last.  Exchanges only on a strictly
+// greater expert, so the order is the insertion sort's.
+template <int KB, typename Coef>
 __device__ __attribute__((always_inline)) inline void token_slots_by_expert(int t, int K,
                                                                            const int32_t* __restrict__ idx,
                                                                            const int32_t* __restrict__ pos,
                                                                            Coef coef, int* e, int* p, float* w) {
 #pragma unroll
-  for (int k = 0; k < kMaxK; ++k) {
+  for (int k = 0; k < KB; ++k) {
     const bool on = k < K;
     e[k] = on ? idx[(int64_t)t * K + k] : INT_MAX;
     p[k] = on && pos ? pos[(int64_t)t * K + k] : 0;
     w[k] = on ? coef((int64_t)t * K + k) : 0.f;
   }
 #pragma unroll
-  for (int i = 0; i < kMaxK - 1; ++i)
+  for (int i = 0; i < KB - 1; ++i)
 #pragma unroll
-    for (int j = 0; j < kMaxK - 1 - i; ++j)
+    for (int j = 0; j < KB - 1 - i; ++j)
       if (e[j] > e[j + 1]) {
         const int te = e[j], tp = p[j];
         const float tw = w[j];
@@ -416,6 +435,41 @@ __device__ __attribute__((always_inline)) inline void token_slots_by_expert(int 
       }
 }
 
+// Runs body(p, e, w) for token t's K slots in ascending-expert order (p: the
+// dispatched row, 0 without pos; w = coef(t*K + k)).  Up to 8 slots the
+// compare-exchange network of token_slots_by_expert sorts them in registers and
+// the loop is unrolled.  Beyond that, lane k holds slot k, finds its place by
+// counting the slots with a smaller expert (a token's experts are distinct),
+// and iteration r reads the slot placed r-th with a ballot and lane shuffles.
+template <int KB, typename Coef, typename Body>
+__device__ __attribute__((always_inline)) inline void for_each_sorted_slot(int t, int K,
+                                                                          const int32_t* __restrict__ idx,
+                                                                          const int32_t* __restrict__ pos, Coef coef,
+                                                                          Body body) {
+  if constexpr (KB <= 8) {
+    int e[KB], p[KB];
+    float w[KB];
+    token_slots_by_expert<KB>(t, K, idx, pos, coef, e, p, w);
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      if (k >= K) break;
+      body(p[k], e[k], w[k]);
+    }
+  } else {
+    const int lane = threadIdx.x & 63;
+    const bool on = lane < K;
+    const int my_e = on ? idx[(int64_t)t * K + lane] : INT_MAX;
+    const int my_p = on && pos ? pos[(int64_t)t * K + lane] : 0;
+    const float my_w = on ? coef((int64_t)t * K + lane) : 0.f;
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += __shfl(my_e, j) < my_e ? 1 : 0;
+    for (int r = 0; r < K; ++r) {
+      const int src = __ffsll((unsigned long long)__ballot(on && rank == r)) - 1;
+      body(__shfl(my_p, src), __shfl(my_e, src), __shfl(my_w, src));
+    }
+  }
+}
+
 // Row vectors per lane whose loads of one slot are in flight together in the
 // wave-per-token gather kernels.
 constexpr int kGatherBatch = 4;
@@ -425,7 +479,7 @@ constexpr int kGatherBatch = 4;
 // fp32 accumulation, one rounding (the stack().sum(0) of moe.py:85).
 // Gather-reduce per token: no atomics, deterministic.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int KB>
 __global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ y, const T* __restrict__ weights,
                                                           const int32_t* __restrict__ idx,
                                                           const int32_t* __restrict__ pos, int T_, int D, int K,
@@ -437,9 +491,7 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ 
   const int lane = threadIdx.x & 63;
   const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (t >= T_) return;
-  int e[kMaxK], p[kMaxK];
-  float w[kMaxK];
-  token_slots_by_expert(t, K, idx, pos, [&](int64_t i) { return to_f32<T>(weights[i]); }, e, p, w);
+  auto coef = [&](int64_t i) { return to_f32<T>(weights[i]); };
   const int nvec = D / VEC;
   for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
     float acc[U][VEC];
@@ -447,20 +499,18 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ 
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[u][i] = 0.f;
-#pragma unroll
-    for (int k = 0; k < kMaxK; ++k) {
-      if (k >= K) break;
+    for_each_sorted_slot<KB>(t, K, idx, pos, coef, [&](int pk, int, float wk) __attribute__((always_inline)) {
       Vec16 v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = c0 + u * 64 + lane;
-        v[u] = c < nvec ? ld16(y + (int64_t)p[k] * D + c * VEC) : zero16();
+        v[u] = c < nvec ? ld16(y + (int64_t)pk * D + c * VEC) : zero16();
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[u][i] += round_to<T>(VecTraits<T>::get(v[u], i) * w[k]);
-    }
+        for (int i = 0; i < VEC; ++i) acc[u][i] += round_to<T>(VecTraits<T>::get(v[u], i) * wk);
+    });
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * 64 + lane;
@@ -493,7 +543,7 @@ __device__ inline void gating_bwd_token(int K, float rho, const float* dw, const
 // written to the dispatched row, dw(t,k) = <dout[t], y(t,k)>, then the
 // sigmoid / renormalise backward to dL/dlogit for the K selected experts.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int KB>
 __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ dout, const T* __restrict__ y,
                                                           const T* __restrict__ weights,
                                                           const float* __restrict__ score,
@@ -506,10 +556,10 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
   const int lane = threadIdx.x & 63;
   const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (t >= T_) return;
-  int p[kMaxK];
-  float w[kMaxK], dw[kMaxK];
+  int p[KB];
+  float w[KB], dw[KB];
 #pragma unroll
-  for (int k = 0; k < kMaxK; ++k) {
+  for (int k = 0; k < KB; ++k) {
     const bool on = k < K;
     p[k] = on ? pos[(int64_t)t * K + k] : 0;
     w[k] = on ? to_f32<T>(weights[(int64_t)t * K + k]) : 0.f;
@@ -524,7 +574,7 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
       g[u] = c < nvec ? ld16(dout + (int64_t)t * D + c * VEC) : zero16();
     }
 #pragma unroll
-    for (int k = 0; k < kMaxK; ++k) {
+    for (int k = 0; k < KB; ++k) {
       if (k >= K) break;
       Vec16 v[U];
 #pragma unroll
@@ -550,10 +600,10 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
     }
   }
 #pragma unroll
-  for (int k = 0; k < kMaxK; ++k)
+  for (int k = 0; k < KB; ++k)
     if (k < K) dw[k] = wave_sum(dw[k]);
   if (lane == 0) {
-    float sc[kMaxK], dl[kMaxK];
+    float sc[KB], dl[KB];
     float sum = 0.f;
     for (int k = 0; k < K; ++k) {
       sc[k] = score[(int64_t)t * K + k];
@@ -660,7 +710,7 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const T* __restrict_
 // combine_fwd_kernel: no barrier between the slot reads and the row reads,
 // kGatherBatch row vectors of a slot in flight per lane.  The sum per element
 // is the block kernel's, in the same order.
-template <typename T>
+template <typename T, int KB>
 __global__ __launch_bounds__(256) void unpermute_bwd_wave_kernel(const T* __restrict__ dxp,
                                                                  const float* __restrict__ dlogit,
                                                                  const int32_t* __restrict__ idx,
@@ -672,9 +722,8 @@ __global__ __launch_bounds__(256) void unpermute_bwd_wave_kernel(const T* __rest
   const int lane = threadIdx.x & 63;
   const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (t >= T_) return;
-  int e[kMaxK], p[kMaxK];
-  float dl[kMaxK];
-  token_slots_by_expert(t, K, idx, dxp ? pos : nullptr, [&](int64_t i) { return dlogit[i]; }, e, p, dl);
+  auto coef = [&](int64_t i) { return dlogit[i]; };
+  const int32_t* pos_or_null = dxp ? pos : nullptr;
   const int nvec = D / VEC;
   for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
     float acc[U][VEC];
@@ -682,15 +731,13 @@ __global__ __launch_bounds__(256) void unpermute_bwd_wave_kernel(const T* __rest
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[u][i] = 0.f;
-#pragma unroll
-    for (int k = 0; k < kMaxK; ++k) {
-      if (k >= K) break;
+    for_each_sorted_slot<KB>(t, K, idx, pos_or_null, coef, [&](int pk, int ek, float dlk) __attribute__((always_inline)) {
       Vec16 xv[U], wv[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int c = c0 + u * 64 + lane;
-        xv[u] = (dxp && c < nvec) ? ld16(dxp + (int64_t)p[k] * D + c * VEC) : zero16();
-        wv[u] = c < nvec ? ld16(wt + (int64_t)e[k] * D + c * VEC) : zero16();
+        xv[u] = (dxp && c < nvec) ? ld16(dxp + (int64_t)pk * D + c * VEC) : zero16();
+        wv[u] = c < nvec ? ld16(wt + (int64_t)ek * D + c * VEC) : zero16();
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -699,9 +746,9 @@ __global__ __launch_bounds__(256) void unpermute_bwd_wave_kernel(const T* __rest
           for (int i = 0; i < VEC; ++i) acc[u][i] += VecTraits<T>::get(xv[u], i);
         }
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[u][i] += dl[k] * VecTraits<T>::get(wv[u], i);
+        for (int i = 0; i < VEC; ++i) acc[u][i] += dlk * VecTraits<T>::get(wv[u], i);
       }
-    }
+    });
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * 64 + lane;
@@ -717,32 +764,70 @@ __global__ __launch_bounds__(256) void unpermute_bwd_wave_kernel(const T* __rest
 
 // ---------------------------------------------------------------------------
 // B6: router weight gradient dW[d, e] = sum_t x[t, d] * dlogit(t, e), with
-// dlogit nonzero only on the K selected experts.  Pass 1: per (d-block,
-// token-chunk) partial sums in LDS columns (one column per thread, no
-// atomics).  Pass 2: fixed-order sum over chunks.
+// dlogit nonzero only on the K selected experts.  Pass 1: per (column block,
+// token chunk) partial sums (no atomics).  Pass 2: fixed-order sum over chunks.
 // ---------------------------------------------------------------------------
+// Partials for any E and D, 64 experts per block (blockIdx.z = expert group):
+// the chunk's dense coefficients for the group sit in LDS; each lane of a wave
+// owns 2 consecutive columns and keeps their 64 accumulators in registers,
+// and the block's 4 waves take 4 x 128 consecutive columns, each over the
+// whole chunk in token order.
+constexpr int kWideGroup = 64;   // experts per block
+constexpr int kWideCols = 512;   // columns per block (4 waves x 64 lanes x 2)
+constexpr int kWideChunkMax = 256;
 template <typename T>
 __global__ __launch_bounds__(256) void router_wgrad_partial_kernel(const T* __restrict__ x,
                                                                    const float* __restrict__ dlogit,
                                                                    const int32_t* __restrict__ idx, int T_, int D,
                                                                    int E, int K, int chunk,
                                                                    float* __restrict__ partial) {
-  __shared__ float acc[kMaxE][256];
+  __shared__ __align__(16) float coef_s[kWideChunkMax][kWideGroup];
   const int tid = threadIdx.x;
-  const int d = blockIdx.x * 256 + tid;
   const int c = blockIdx.y;
-  for (int e = 0; e < E; ++e) acc[e][tid] = 0.f;
+  const int g0 = blockIdx.z * kWideGroup;
+  const int ng = min(kWideGroup, E - g0);
   const int ta = c * chunk;
-  const int tb = min(T_, ta + chunk);
-  if (d < D) {
-    for (int t = ta; t < tb; ++t) {
-      const float xv = to_f32<T>(x[(int64_t)t * D + d]);
-      for (int k = 0; k < K; ++k) {
-        const int e = idx[(int64_t)t * K + k];
-        acc[e][tid] += xv * dlogit[(int64_t)t * K + k];
-      }
+  const int n = max(0, min(T_, ta + chunk) - ta);
+  for (int i = tid; i < n * kWideGroup; i += 256) coef_s[i / kWideGroup][i % kWideGroup] = 0.f;
+  __syncthreads();
+  for (int i = tid; i < n * K; i += 256) {
+    const int t = i / K;
+    const int e = idx[(int64_t)(ta + t) * K + i % K] - g0;
+    if (e >= 0 && e < ng) coef_s[t][e] = dlogit[(int64_t)(ta + t) * K + i % K];  // a token's experts are distinct
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6;
+  const int d0 = blockIdx.x * kWideCols + w * 128 + lane * 2;
+  if (d0 >= D) return;
+  const bool two = d0 + 1 < D;
+  float acc[kWideGroup][2];
+#pragma unroll
+  for (int e = 0; e < kWideGroup; ++e) acc[e][0] = acc[e][1] = 0.f;
+  const T* xp = x + (int64_t)ta * D + d0;
+  for (int t = 0; t < n; ++t) {
+    const float x0 = to_f32<T>(xp[(int64_t)t * D]);
+    const float x1 = two ? to_f32<T>(xp[(int64_t)t * D + 1]) : 0.f;
+    const float4* cr = reinterpret_cast<const float4*>(coef_s[t]);
+#pragma unroll
+    for (int q = 0; q < kWideGroup / 4; ++q) {
+      const float4 cf = cr[q];
+      acc[4 * q][0] += x0 * cf.x;
+      acc[4 * q][1] += x1 * cf.x;
+      acc[4 * q + 1][0] += x0 * cf.y;
+      acc[4 * q + 1][1] += x1 * cf.y;
+      acc[4 * q + 2][0] += x0 * cf.z;
+      acc[4 * q + 2][1] += x1 * cf.z;
+      acc[4 * q + 3][0] += x0 * cf.w;
+      acc[4 * q + 3][1] += x1 * cf.w;
     }
-    for (int e = 0; e < E; ++e) partial[((int64_t)c * E + e) * D + d] = acc[e][tid];
+  }
+#pragma unroll
+  for (int e = 0; e < kWideGroup; ++e) {
+    if (e < ng) {
+      float* out = partial + ((int64_t)c * E + g0 + e) * D + d0;
+      out[0] = acc[e][0];
+      if (two) out[1] = acc[e][1];
+    }
   }
 }
 
@@ -972,7 +1057,12 @@ void launch_transpose(const void* w, void* wt, int D, int E, int E_pad, hipStrea
                      E_pad);
 }
 
-inline int e_pad(int64_t E) { return (int)((E + 15) / 16) * 16; }
+// Experts of the router kernel instance for E (a multiple of 16: 16, 32, 48,
+// 64, 128 or 256): the rows of the transposed router weights, zero beyond E.
+inline int e_pad(int64_t E) {
+  const int p = (int)((E + 15) / 16) * 16;
+  return p <= 64 ? p : (p <= 128 ? 128 : 256);
+}
 
 // The allocation-free router weight gradient's partial sums: a static device
 // array, one copy per GPU, held until the process ends.  Host code must never
@@ -1008,6 +1098,17 @@ float* scratch_ptr() {
   return g_scratch_dev[dev];
 }
 
+// Calls f(std::integral_constant<int, KB>) with KB = K rounded up to 1, 2, 4,
+// 8 or 16: the slot bound of the wave-per-token gather kernels.
+template <typename F>
+void with_slot_bound(int64_t K, F&& f) {
+  if (K <= 1) f(std::integral_constant<int, 1>());
+  else if (K <= 2) f(std::integral_constant<int, 2>());
+  else if (K <= 4) f(std::integral_constant<int, 4>());
+  else if (K <= 8) f(std::integral_constant<int, 8>());
+  else f(std::integral_constant<int, 16>());
+}
+
 }  // namespace
 
 extern "C" {
@@ -1039,7 +1140,9 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
     case 1: ROUTER_LAUNCH(TT, 1); break; \
     case 2: ROUTER_LAUNCH(TT, 2); break; \
     case 3: ROUTER_LAUNCH(TT, 3); break; \
-    default: ROUTER_LAUNCH(TT, 4); break; \
+    case 4: ROUTER_LAUNCH(TT, 4); break; \
+    case 8: ROUTER_LAUNCH(TT, 8); break; \
+    default: ROUTER_LAUNCH(TT, 16); break; \
   }
   if (dtype == kBF16) {
     ROUTER_DISPATCH_NF(uint16_t)
@@ -1105,12 +1208,15 @@ int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32
   hipStream_t s = (hipStream_t)stream;
   ABACUS_CHECK_ARG(T <= (int64_t)INT_MAX - 3, "too many tokens (%lld)", (long long)T);
   const unsigned grid = (unsigned)((T + 3) / 4);  // a token per wave
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(combine_fwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)y_RD,
-                       (const uint16_t*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (uint16_t*)out_TD);
-  else
-    hipLaunchKernelGGL(combine_fwd_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)y_RD,
-                       (const float*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (float*)out_TD);
+  with_slot_bound(K, [&](auto kb) {
+    constexpr int KB = decltype(kb)::value;
+    if (dtype == kBF16)
+      hipLaunchKernelGGL((combine_fwd_kernel<uint16_t, KB>), dim3(grid), dim3(256), 0, s, (const uint16_t*)y_RD,
+                         (const uint16_t*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (uint16_t*)out_TD);
+    else
+      hipLaunchKernelGGL((combine_fwd_kernel<float, KB>), dim3(grid), dim3(256), 0, s, (const float*)y_RD,
+                         (const float*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (float*)out_TD);
+  });
   ABACUS_CHECK_LAUNCH("combine_fwd");
   return 0;
 }
@@ -1123,14 +1229,17 @@ int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* we
   hipStream_t s = (hipStream_t)stream;
   ABACUS_CHECK_ARG(T <= (int64_t)INT_MAX - 3, "too many tokens (%lld)", (long long)T);
   const unsigned grid = (unsigned)((T + 3) / 4);  // a token per wave
-  if (dtype == kBF16)
-    hipLaunchKernelGGL(combine_bwd_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)dout_TD,
-                       (const uint16_t*)y_RD, (const uint16_t*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
-                       route_scale, (uint16_t*)dy_RD, dlogit_TK);
-  else
-    hipLaunchKernelGGL(combine_bwd_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)dout_TD,
-                       (const float*)y_RD, (const float*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
-                       route_scale, (float*)dy_RD, dlogit_TK);
+  with_slot_bound(K, [&](auto kb) {
+    constexpr int KB = decltype(kb)::value;
+    if (dtype == kBF16)
+      hipLaunchKernelGGL((combine_bwd_kernel<uint16_t, KB>), dim3(grid), dim3(256), 0, s, (const uint16_t*)dout_TD,
+                         (const uint16_t*)y_RD, (const uint16_t*)weights_TK, score_TK, pos_TK, (int)T, (int)D,
+                         (int)K, route_scale, (uint16_t*)dy_RD, dlogit_TK);
+    else
+      hipLaunchKernelGGL((combine_bwd_kernel<float, KB>), dim3(grid), dim3(256), 0, s, (const float*)dout_TD,
+                         (const float*)y_RD, (const float*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
+                         route_scale, (float*)dy_RD, dlogit_TK);
+  });
   ABACUS_CHECK_LAUNCH("combine_bwd");
   return 0;
 }
@@ -1168,13 +1277,17 @@ int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, con
   }
   if (D % (dtype == kBF16 ? 8 : 4) == 0 && T <= (int64_t)INT_MAX - 3) {
     const unsigned wgrid = (unsigned)((T + 3) / 4);
-    if (dtype == kBF16)
-      hipLaunchKernelGGL(unpermute_bwd_wave_kernel<uint16_t>, dim3(wgrid), dim3(256), 0, s,
-                         (const uint16_t*)dx_perm_RD, dlogit_TK, idx_TK, pos_TK, (const uint16_t*)wt_ws, (int)T,
-                         (int)D, (int)K, (uint16_t*)dx_TD);
-    else
-      hipLaunchKernelGGL(unpermute_bwd_wave_kernel<float>, dim3(wgrid), dim3(256), 0, s, (const float*)dx_perm_RD,
-                         dlogit_TK, idx_TK, pos_TK, (const float*)wt_ws, (int)T, (int)D, (int)K, (float*)dx_TD);
+    with_slot_bound(K, [&](auto kb) {
+      constexpr int KB = decltype(kb)::value;
+      if (dtype == kBF16)
+        hipLaunchKernelGGL((unpermute_bwd_wave_kernel<uint16_t, KB>), dim3(wgrid), dim3(256), 0, s,
+                           (const uint16_t*)dx_perm_RD, dlogit_TK, idx_TK, pos_TK, (const uint16_t*)wt_ws, (int)T,
+                           (int)D, (int)K, (uint16_t*)dx_TD);
+      else
+        hipLaunchKernelGGL((unpermute_bwd_wave_kernel<float, KB>), dim3(wgrid), dim3(256), 0, s,
+                           (const float*)dx_perm_RD, dlogit_TK, idx_TK, pos_TK, (const float*)wt_ws, (int)T, (int)D,
+                           (int)K, (float*)dx_TD);
+    });
     ABACUS_CHECK_LAUNCH("unpermute_bwd");
     return 0;
   }
@@ -1197,9 +1310,10 @@ static int wgrad_cpt(int dtype) { return dtype == kBF16 ? 8 : 4; }
 static bool router_wgrad_reg_path(int64_t D, int64_t E, int dtype) { return E <= 16 && D % wgrad_cpt(dtype) == 0; }
 
 // Token chunks of the partial pass: enough blocks to fill the GPU (~512),
-// partials of at most half the bytes of x, at most kWgradChunkMax tokens.
+// partials of at most half the bytes of x, at most kWgradChunkMax (register
+// path) or kWideChunkMax (wide path) tokens.
 static void router_wgrad_plan(int64_t T, int64_t D, int64_t E, int dtype, bool reg, int* chunk, int* nchunks) {
-  const int64_t cols_per_block = reg ? 64 * wgrad_cpt(dtype) : 256;
+  const int64_t cols_per_block = reg ? 64 * wgrad_cpt(dtype) : kWideCols;
   const int64_t dblocks = (D + cols_per_block - 1) / cols_per_block;
   const int64_t elem = dtype == kBF16 ? 2 : 4;
   int64_t nc = std::max<int64_t>(1, 512 / dblocks);
@@ -1208,6 +1322,7 @@ static void router_wgrad_plan(int64_t T, int64_t D, int64_t E, int dtype, bool r
   int64_t ch = (T + nc - 1) / nc;
   if (ch < 1) ch = 1;
   if (reg && ch > kWgradChunkMax) ch = kWgradChunkMax;
+  if (!reg && ch > kWideChunkMax) ch = kWideChunkMax;
   *chunk = (int)ch;
   *nchunks = (int)std::max<int64_t>(1, (T + ch - 1) / ch);
 }
@@ -1243,14 +1358,15 @@ static int router_wgrad_launch(const void* x_TD, const float* dlogit_TK, const i
       else ABACUS_WGRAD_REG(float, 16);
     }
 #undef ABACUS_WGRAD_REG
-  } else if (dtype == kBF16) {
-    const dim3 g1((unsigned)((D + 255) / 256), (unsigned)nchunks);
-    hipLaunchKernelGGL(router_wgrad_partial_kernel<uint16_t>, g1, dim3(256), 0, s, (const uint16_t*)x_TD,
-                       dlogit_TK, idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
   } else {
-    const dim3 g1((unsigned)((D + 255) / 256), (unsigned)nchunks);
-    hipLaunchKernelGGL(router_wgrad_partial_kernel<float>, g1, dim3(256), 0, s, (const float*)x_TD, dlogit_TK,
-                       idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
+    const dim3 g1((unsigned)((D + kWideCols - 1) / kWideCols), (unsigned)nchunks,
+                  (unsigned)((E + kWideGroup - 1) / kWideGroup));
+    if (dtype == kBF16)
+      hipLaunchKernelGGL(router_wgrad_partial_kernel<uint16_t>, g1, dim3(256), 0, s, (const uint16_t*)x_TD,
+                         dlogit_TK, idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
+    else
+      hipLaunchKernelGGL(router_wgrad_partial_kernel<float>, g1, dim3(256), 0, s, (const float*)x_TD, dlogit_TK,
+                         idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
   }
   ABACUS_CHECK_LAUNCH("router_wgrad_partial");
   if ((E * D) % 4 == 0) {

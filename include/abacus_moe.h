@@ -16,8 +16,8 @@
  *     fp32.
  *   - Return 0 on success, nonzero on a rejected argument (1) or launch
  *     failure (2); abacus_moe_last_error() gives the message (per thread).
- *   - Sizes: T tokens, D model dim, E experts (<= 64), K slots per token
- *     (<= 8), M expert hidden dim, R = T*K routed rows.  D and M must be
+ *   - Sizes: T tokens, D model dim, E experts (<= 256), K slots per token
+ *     (<= 16), M expert hidden dim, R = T*K routed rows.  D and M must be
  *     multiples of 8 (bf16) or 4 (fp32).
  *   - offsets_E1[e] .. offsets_E1[e+1] are the routed rows of expert e in every
  *     expert-contiguous (R, .) buffer; rows are expert-major and, inside an

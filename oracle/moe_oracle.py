@@ -14,6 +14,8 @@ Pinning (tests/test_oracle.py):
   sigmoid_cr            - fp64 closed form vs math.exp; within 2 ulp (fp32) / 1 ulp (bf16)
                           of torch.sigmoid, which is itself not correctly rounded
   topk_canonical        - torch.topk on tie-free rows; brute-force ranking on tiny inputs
+  sum_in_pick_order     - torch.sum: equal for K = 1-4 and 8, within 2(K-1) ulp otherwise;
+                          a Python fp64 loop rounded per step on tiny inputs
   dispatch              - brute-force restatement of the expert loop; torch.argsort(stable)
   bias_step             - the reference's known-answer test (router.py test: [-10, 10, 0, 10])
   router_forward        - the reference's known-answer test (indices [2, .], then [3, 1])
@@ -29,6 +31,12 @@ Parity pinned this way for every function above; nothing is left "unpinned".
 Tie rule (the reference leaves it to torch.topk, whose order among equal values
 is implementation-defined): descending selection value, ties -> lower expert
 index, NaN above every number.
+
+Sum order of the K picked scores (the reference leaves it to torch.sum, whose
+order is implementation-defined for K >= 5): left to right in pick order, fp32
+accumulation for 16-bit dtypes, one rounding (sum_in_pick_order).  Pinned
+against torch.sum: equal for K = 1-4 and 8, within 2(K-1) ulp of the sum for
+other K.
 """
 
 from __future__ import annotations
@@ -98,9 +106,23 @@ def route(logits: torch.Tensor, bias_E: torch.Tensor, top_k: int, route_scale: f
     scores = sigmoid_cr(logits)
     indices = topk_canonical(selection(scores, bias_E), top_k)
     picked = scores.gather(dim=-1, index=indices)
-    weights = picked / picked.sum(dim=-1, keepdim=True)
+    weights = picked / sum_in_pick_order(picked)
     weights = weights * route_scale
     return weights, indices, scores
+
+
+def sum_in_pick_order(picked: torch.Tensor) -> torch.Tensor:
+    """The renormalisation's denominator (router.py:49), keepdim: the K picked scores added left to
+    right in pick order, in fp32 for 16-bit dtypes (torch's accumulation type there), rounded once
+    to the dtype.  torch.sum's order over K terms is implementation-defined: on the CPU it adds
+    1-4 and 8 terms left to right and 5-7 and 9 or more in another order, so for those K the
+    reference's own results differ from run to run of the implementation by up to 2(K-1) ulp of
+    the sum."""
+    acc_dtype = torch.float32 if picked.dtype in (torch.bfloat16, torch.float16) else picked.dtype
+    acc = picked[..., :1].to(acc_dtype)
+    for k in range(1, picked.shape[-1]):
+        acc = acc + picked[..., k:k + 1].to(acc_dtype)
+    return acc.to(picked.dtype)
 
 
 def bias_step(bias_E: torch.Tensor, indices: torch.Tensor, n_experts: int, speed: float) -> torch.Tensor:
@@ -179,7 +201,7 @@ def moe_forward(
     if indices_TK is None:
         indices_TK = topk_canonical(selection(scores, bias_E), top_k)
     picked = scores.gather(dim=-1, index=indices_TK)
-    weights = picked / picked.sum(dim=-1, keepdim=True) * route_scale
+    weights = picked / sum_in_pick_order(picked) * route_scale
     if x_TD.shape[0] == 0:
         return x_TD, indices_TK
     parts = []

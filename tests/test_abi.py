@@ -72,7 +72,8 @@ def test_abi_version_and_queries():
 @pytest.mark.parametrize(
     "name,args,msg",
     [
-        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 65, 2, 1.0, 1) + (None,) * 8, "n_experts"),
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 257, 2, 1.0, 1) + (None,) * 8, "n_experts"),
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 64, 17, 1.0, 1) + (None,) * 8, "top_k"),
         ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 9, 1.0, 1) + (None,) * 8, "top_k"),
         ("abacus_moe_permute_gather", (None, None, None, 16, 12, 8, 2, 1, None, None, None, None), "dim"),
         ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 2, 1.0, 7) + (None,) * 8, "dtype"),

@@ -4,7 +4,8 @@ The reference's own CPU tests, restated: the router's known answer (tests/test_m
 expert equal to the dense MLP (tests/test_moe.py:42-53) and MoEExpertParallel in one process equal
 to MoE (tests/test_moe_ep.py:14-23).  Then the layer's forward and backward against the oracle
 (router.py:40-70, moe.py:60-86 restated), routing bit-exact given the library's logits, in fp32 and
-bf16 and at shapes the GPU kernels do not take (E > 64, K > 8, D not a multiple of 8); the
+bf16, with more than 64 experts and 8 slots and with D not a multiple of 8 (which the GPU kernels
+reject); the
 load-balancing loss; and the decoder's MoE blocks.  The host library is checked to be the code that
 ran: the oracle is never on the product path.
 """
@@ -20,6 +21,7 @@ from abacus.moe.router import Router
 from abacus_amd import _lib
 from abacus_amd import workloads as W
 from oracle import moe_oracle as oracle
+from special_selection import SPECIAL_CASES, check_special_selection
 
 
 def test_router_known_answer():
@@ -105,10 +107,7 @@ def test_layer_matches_oracle(T, D, E, K, M, dtype):
     # routing: bit-exact against the oracle given the library's logits; counts, offsets, permutation
     w_o, idx_o, _ = oracle.route(r.logits_TE, bias0, K, moe.router.route_scale)
     assert torch.equal(r.indices_TK, idx_o)
-    if K <= 8:
-        assert torch.equal(r.weights_TK, w_o)
-    else:  # the K picked scores are summed in pick order; torch's sum of more than 8 takes another order
-        torch.testing.assert_close(r.weights_TK, w_o, rtol=2.5e-7, atol=0.0)
+    assert torch.equal(r.weights_TK, w_o)
     counts, offsets, perm, pos = oracle.dispatch(idx_o, E)
     assert np.array_equal(r.counts_E.numpy(), counts) and np.array_equal(r.offsets_E1.numpy(), offsets)
     assert np.array_equal(r.perm_R.numpy(), perm) and np.array_equal(r.pos_TK.numpy(), pos)
@@ -232,3 +231,9 @@ def test_adamw_on_cpu_matches_oracle(dtype):
     for p, o in zip(model, ora):
         got, want = p.detach().double().numpy(), o[0].astype(np.float64)
         assert np.all(np.abs(got - want) <= ulp * np.abs(want) + 1e-30)
+
+
+@pytest.mark.parametrize("E,K,dtype", SPECIAL_CASES, ids=[f"E{e}_K{k}_{str(d)[6:]}" for e, k, d in SPECIAL_CASES])
+def test_selection_order_special_values_on_cpu(E, K, dtype):
+    """NaN, +-inf, exact ties and zero selections on the host build: see tests/special_selection.py."""
+    check_special_selection(E, K, dtype, torch.device("cpu"))

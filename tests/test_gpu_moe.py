@@ -230,6 +230,41 @@ def test_bf16_odd_shapes(T, D, M, E, K):
     check_against(moe, x, target, torch.device("cpu"))
 
 
+@pytest.mark.parametrize("T,D,M,E,K,dtype", [
+    (300, 256, 128, 128, 8, torch.bfloat16),
+    (200, 128, 64, 256, 16, torch.float32),
+    (500, 512, 256, 80, 10, torch.bfloat16),
+    (257, 64, 96, 65, 1, torch.float32),
+], ids=["E128_K8_bf16", "E256_K16_f32", "E80_K10_bf16", "E65_K1_f32"])
+def test_wide_expert_counts(T, D, M, E, K, dtype):
+    """Router sizes beyond 64 experts and 8 slots (up to the library's 256 and 16; the reference's
+    Router takes any E >= 1, 1 <= K <= E, router.py:25-28): routing bit-exact against the oracle
+    on the kernel's logits, then the layer against the oracle."""
+    print(f"\n[moe-wide] T={T} D={D} M={M} E={E} K={K} {dtype}", flush=True)
+    torch.manual_seed(E + K)
+    moe = MoE(D, E, K, hidden_dim=M)
+    with torch.no_grad():
+        for p in (moe.router.w_DE, moe.w_gate_EDM, moe.w_up_EDM, moe.w_down_EMD):
+            p.normal_(0.0, 0.05)
+    moe = moe.to(DEV, dtype)
+    x = torch.randn(T, D, device=DEV).to(dtype)
+    target = torch.randn(T, D, device=DEV).to(dtype)
+    moe.train()
+    bias0 = moe.router.expert_bias_E.detach().clone()
+    with torch.no_grad():
+        moe(x)
+    torch.cuda.synchronize()
+    r = moe.router.last_routing
+    w_o, idx_o, _ = oracle.route(r.logits_TE.cpu(), bias0.cpu(), K, moe.router.route_scale)
+    assert torch.equal(r.indices_TK.cpu(), idx_o)
+    assert torch.equal(r.weights_TK.cpu(), w_o)
+    counts, offsets, perm, pos = oracle.dispatch(idx_o, E)
+    assert r.counts_E.cpu().tolist() == counts.tolist() and r.offsets_E1.cpu().tolist() == offsets.tolist()
+    assert r.perm_R.cpu().tolist() == perm.tolist() and r.pos_TK.cpu().reshape(-1).tolist() == pos.reshape(-1).tolist()
+    assert torch.equal(moe.router.expert_bias_E.cpu(), oracle.bias_step(bias0.cpu(), idx_o, E, moe.router.bias_update_speed))
+    check_against(moe, x, target, torch.device("cpu"))
+
+
 def test_two_training_steps_track_bias_updates():
     """Two train-mode iterations (tests/test_moe_ep.py:49-71): outputs, grads and the bias."""
     torch.manual_seed(1)

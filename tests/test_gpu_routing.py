@@ -12,6 +12,7 @@ from abacus_amd import workloads as W
 from abacus.moe.router import Router
 from oracle import moe_oracle as oracle
 from routing_check import check_against_torch_topk
+from special_selection import SPECIAL_CASES, check_special_selection
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -127,3 +128,11 @@ def test_update_bias_explicit_indices():
     idx = torch.tensor([[0, 1], [0, 2], [0, 1]], device=DEV)
     router.update_bias(idx)
     assert router.expert_bias_E.tolist() == [-0.5, -0.5, 0.5, 0.5]
+
+
+
+@pytest.mark.parametrize("E,K,dtype", SPECIAL_CASES, ids=[f"E{e}_K{k}_{str(d)[6:]}" for e, k, d in SPECIAL_CASES])
+def test_selection_order_special_values(E, K, dtype):
+    """NaN, +-inf, exact ties and zero selections: see tests/special_selection.py."""
+    print(f"\n[routing-special] E={E} K={K} {dtype}", flush=True)
+    check_special_selection(E, K, dtype, DEV)

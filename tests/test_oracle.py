@@ -108,6 +108,29 @@ def test_topk_canonical_tie_rule_bruteforce():
         assert got[r].tolist() == key[:3]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sum_in_pick_order(dtype):
+    """The renormalisation denominator: a per-step-rounded Python loop (fp32 accumulation, one
+    rounding to the dtype) on small rows; torch.sum equal where it adds left to right (K = 1-4
+    and 8 on the CPU) and within 2(K-1) ulp of the sum for every K."""
+    gen = torch.Generator().manual_seed(5)
+    for K in range(1, 17):
+        picked = torch.rand(300, K, generator=gen).to(dtype)
+        got = oracle.sum_in_pick_order(picked)
+        assert got.shape == (300, 1) and got.dtype == dtype
+        for r in range(20):
+            acc = np.float32(0.0)
+            for v in picked[r].float().tolist():
+                acc = np.float32(acc + np.float32(v))
+            assert float(got[r, 0]) == float(torch.tensor(float(acc)).to(dtype)), (K, r)
+        want = picked.sum(dim=-1, keepdim=True)
+        if K in (1, 2, 3, 4, 8):
+            assert torch.equal(got, want), K
+        u = 2.0 ** -24 if dtype == torch.float32 else 2.0 ** -8
+        tol = (2 * max(K - 1, 0) * 2.0 ** -24 + 2 * u) * want.double().abs()
+        assert bool(((got.double() - want.double()).abs() <= tol).all()), K
+
+
 def test_dispatch_matches_bruteforce_and_stable_argsort():
     gen = torch.Generator().manual_seed(4)
     for T, E, K in [(1, 4, 1), (7, 4, 2), (33, 8, 3), (64, 16, 6)]:
