@@ -85,9 +85,9 @@ __device__ inline uint64_t selection_key(float v, int e) {
 // ---------------------------------------------------------------------------
 // K1: fused router.  One block = 16 tokens x all experts; the 4 waves split
 // the D reduction (k-blocks interleaved), partials are summed in LDS in a
-// fixed order, the sigmoid and bias are applied per (token, expert), then one
-// wave per token runs the top-k / renormalise epilogue and bumps the block's
-// expert histogram.
+// fixed order, the sigmoid and bias are applied per (token, expert), then
+// 16-64 lanes per token run the top-k / renormalise epilogue and bump the
+// block's expert histogram.
 // ---------------------------------------------------------------------------
 template <typename T, int NF>
 __global__ __launch_bounds__(256) void router_fwd_kernel(
@@ -185,18 +185,23 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   }
   __syncthreads();
 
-  // Top-K, one wave per token (4 tokens per wave): lane l holds experts l,
-  // l + 64, ... as selection keys; each of the K rounds takes the wave maximum
-  // key and retires that expert.
-  constexpr int CPL = EP <= 64 ? 1 : EP / 64;  // experts per lane
-  for (int tok = wave; tok < kRouteTB; tok += 4) {
+  // Top-K: L lanes per token (L = 16, 32 or 64 as EP allows; 64 / L tokens
+  // per wave at once), lane j of a token holding experts j, j + L, ... as
+  // selection keys.  Each of the K rounds takes the maximum key over the
+  // token's lanes and retires that expert.
+  constexpr int L = EP >= 64 ? 64 : (EP <= 16 ? 16 : (EP <= 32 ? 32 : 64));
+  constexpr int TPW = 64 / L;                  // tokens per wave pass
+  constexpr int CPL = EP <= L ? 1 : EP / L;    // experts per lane
+  const int sub = lane / L, ln = lane % L;
+  for (int tok0 = wave * TPW; tok0 < kRouteTB; tok0 += 4 * TPW) {
+    const int tok = tok0 + sub;
     const int t = t0 + tok;
-    if (t >= T_) break;  // the same for the whole wave
+    const bool valid = t < T_;
     uint64_t key[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      const int e = lane + 64 * c;
-      key[c] = e < E ? selection_key(s_sel[tok][e], e) : 0ull;
+      const int e = ln + L * c;
+      key[c] = valid && e < E ? selection_key(s_sel[tok][e], e) : 0ull;
     }
     float sum = 0.f, my_s = 0.f;
     int my_e = 0;
@@ -205,28 +210,28 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
 #pragma unroll
       for (int c = 1; c < CPL; ++c) best = key[c] > best ? key[c] : best;
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)best, off, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64);
+      for (int off = L / 2; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)best, off, L);
+        const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, L);
         const uint64_t o = ((uint64_t)hi << 32) | lo;
         best = o > best ? o : best;
       }
-      const int be = (int)(~(uint32_t)best);
+      const int be = valid ? (int)(~(uint32_t)best) : 0;
 #pragma unroll
       for (int c = 0; c < CPL; ++c)
-        if (lane + 64 * c == be) key[c] = 0ull;
+        if (ln + L * c == be) key[c] = 0ull;
       const float sc = s_sc[tok][be];
       sum += sc;  // pick order
-      if (lane == k) {
+      if (ln == k) {
         my_s = sc;
         my_e = be;
       }
-      if (lane == 0) atomicAdd(&s_cnt[be], 1);
+      if (valid && ln == 0) atomicAdd(&s_cnt[be], 1);
     }
-    if (lane < K) {
+    if (valid && ln < K) {
       const float denom = round_to<T>(sum);
       const float w = round_to<T>(round_to<T>(my_s / denom) * route_scale);
-      const int64_t o = (int64_t)t * K + lane;
+      const int64_t o = (int64_t)t * K + ln;
       weights[o] = from_f32<T>(w);
       indices[o] = my_e;
       idx32[o] = my_e;
