@@ -134,14 +134,22 @@ HOST = _HostStream()
 
 
 class KernelTimer:
-    """Records a pair of HIP events around every entry-point call made while active.
+    """Records a pair of HIP events around every entry-point call made while active
+    (or only around the calls of the entry points named in `only`).
 
     The events go to torch's current stream, which is the stream every entry
-    point is launched on, so (end - start) is that call's device time.
+    point is launched on, so (end - start) is that call's device time.  Each
+    event record is a packet of its own between two kernels and delays the
+    next one by a few microseconds, so a timer that names only the kernel it
+    needs perturbs the surrounding time least.
     """
 
-    def __init__(self) -> None:
+    def __init__(self, only: set[str] | None = None) -> None:
         self.events: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+        self.only = only
+
+    def wants(self, name: str) -> bool:
+        return self.only is None or name in self.only
 
     def __enter__(self) -> "KernelTimer":
         global _timer
@@ -178,7 +186,7 @@ def call(name: str, *args) -> None:
             raise RuntimeError(f"{name} failed ({rc}): {msg}")
         return
     lib = load()
-    timer = _timer
+    timer = _timer if _timer is not None and _timer.wants(name) else None
     if timer is not None:
         start = torch.cuda.Event(enable_timing=True)
         start.record()
