@@ -665,6 +665,94 @@ __host__ __device__ inline int expert_row_tiles(int rows, int thin) {
   return BMT == BM ? rows / BM + (rem > THIN ? 1 : 0) : (rem > 0 && rem <= THIN ? 1 : 0);
 }
 
+// The row tiles of a row-grouped launch, indexed once per work-group in LDS:
+// the expert offsets and, per tile class (0: full, 1: thin), the exclusive
+// prefix over experts of their row tiles ([E] = the class's total).  A block
+// then finds its tile by a binary search in LDS instead of walking the
+// offsets in global memory (which cost the blocks of the host's upper bound
+// that find no tile several microseconds each).
+struct RowIndex {
+  const int* offs;
+  const int* cum[2];
+  int total[2];
+};
+
+// All threads of the work-group call it.  offs_s: E + 1 ints; cum_s: two
+// arrays of E + 1 ints.
+template <int NTH>
+__device__ inline RowIndex build_row_index(const GemmArgs& g, int* offs_s, int* cum_f, int* cum_t) {
+  __shared__ int wsum[2][NTH / 64];
+  const int E = g.E, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int i = tid; i <= E; i += NTH) offs_s[i] = g.offsets[i];
+  __syncthreads();
+  const int per = (E + NTH - 1) / NTH;
+  const int i0 = min(E, tid * per), i1 = min(E, i0 + per);
+  int f = 0, t = 0;
+  for (int i = i0; i < i1; ++i) {
+    const int rows = offs_s[i + 1] - offs_s[i];
+    f += expert_row_tiles<BM>(rows, g.thin);
+    t += expert_row_tiles<THIN>(rows, g.thin);
+  }
+  int fi = f, ti = t;  // inclusive scan over the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int a = __shfl_up(fi, o, 64), c = __shfl_up(ti, o, 64);
+    if (lane >= o) {
+      fi += a;
+      ti += c;
+    }
+  }
+  if (lane == 63) {
+    wsum[0][wave] = fi;
+    wsum[1][wave] = ti;
+  }
+  __syncthreads();
+  int pf = fi - f, pt = ti - t;  // exclusive, then plus the earlier waves
+  for (int w = 0; w < wave; ++w) {
+    pf += wsum[0][w];
+    pt += wsum[1][w];
+  }
+  for (int i = i0; i < i1; ++i) {
+    cum_f[i] = pf;
+    cum_t[i] = pt;
+    const int rows = offs_s[i + 1] - offs_s[i];
+    pf += expert_row_tiles<BM>(rows, g.thin);
+    pt += expert_row_tiles<THIN>(rows, g.thin);
+  }
+  if (tid == NTH - 1) {
+    cum_f[E] = pf;
+    cum_t[E] = pt;
+  }
+  __syncthreads();
+  RowIndex ri;
+  ri.offs = offs_s;
+  ri.cum[0] = cum_f;
+  ri.cum[1] = cum_t;
+  ri.total[0] = cum_f[E];
+  ri.total[1] = cum_t[E];
+  return ri;
+}
+
+// Row tile mt of class BMT -> its expert and rows (as find_row_tile), by a
+// binary search for the last expert whose prefix is at most mt.
+template <int BMT>
+__device__ inline bool find_row_tile(const RowIndex& ri, int E, int mt, int& e, int& row0, int& row_end) {
+  constexpr int c = BMT == BM ? 0 : 1;
+  const int* cum = ri.cum[c];
+  if (mt < 0 || mt >= ri.total[c]) return false;
+  int lo = 0, hi = E - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cum[mid] <= mt) lo = mid;
+    else hi = mid - 1;
+  }
+  e = lo;
+  const int a = ri.offs[e], b = ri.offs[e + 1];
+  row0 = BMT == BM ? a + (mt - cum[e]) * BM : a + (b - a) / BM * BM;
+  row_end = b;
+  return true;
+}
+
 template <int BMT>
 __device__ inline int count_row_tiles(const GemmArgs& g) {
   int n = 0;
@@ -757,7 +845,8 @@ __device__ inline TileId tile_of_logical(int L, int MTp, int NTp) {
 // multiple of 8, so b % 8 is still the XCD the block runs on when a launch
 // runs several kinds back to back).  lds: the work-group's LDS_BYTES.
 template <int KIND, int BMT = BM>
-__device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& g, int b, int G, char* lds) {
+__device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& g, int b, int G, char* lds,
+                                                                const RowIndex* ri) {
   using KT = KindTraits<KIND>;
   using Op = MfmaOp<uint16_t, 32>;
   using GE = Geo<BMT>;
@@ -777,7 +866,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   int part = -1, slot = 0;  // slice of a split tail tile, its workspace slot
   TileId tl;
   if (!KT::WGRAD) {
-    const int mt_real = count_row_tiles<BMT>(g);
+    const int mt_real = ri->total[BMT == BM ? 0 : 1];
     const int total = mt_real * g.tiles_n;
     int r;
     if (!block_to_row_tile(g, b, total, r, part)) return;
@@ -790,7 +879,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   n0 = tl.nt * BNH;
   if (n0 >= g.Ndim) return;
   if (!KT::WGRAD) {
-    if (!find_row_tile<BMT>(g, tl.mt, e, row0, row_end)) return;
+    if (!find_row_tile<BMT>(*ri, g.E, tl.mt, e, row0, row_end)) return;
     k_len = g.Kdim;
   } else {
     e = tl.e;
@@ -816,7 +905,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // a slice of a split tile runs k-tiles kbase .. kbase + ktiles - 1
   int kbase = 0, ktiles = ktiles_all;
   if (part >= 0) {
-    const int S = split_slices(g, count_row_tiles<BMT>(g) * g.tiles_n % g.split_cus);
+    const int S = split_slices(g, ri->total[BMT == BM ? 0 : 1] * g.tiles_n % g.split_cus);
     const int per = (ktiles_all + S - 1) / S;
     kbase = part * per;
     ktiles = max(0, min(per, ktiles_all - kbase));
@@ -1371,15 +1460,16 @@ template <int KR, int KW>
 __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, GemmArgs g2, GemmArgs g3, int n1,
                                                                int n2) {
   __shared__ __attribute__((aligned(1024))) char lds[LDS_ALLOC];
+  __shared__ int offs_s[kMaxExperts + 1];
   const int b = blockIdx.x;
-  if (b < n1) {
-    gemm_tile<KR, BM>(g1, b, n1, lds);
-  } else if (b < n1 + n2) {
-    gemm_tile<KR, THIN>(g2, b - n1, n2, lds);
+  if (b < n1 + n2) {
+    __shared__ int cum_s[2][kMaxExperts + 1];
+    const RowIndex ri = build_row_index<NT>(g1, offs_s, cum_s[0], cum_s[1]);
+    if (b < n1) gemm_tile<KR, BM>(g1, b, n1, lds, &ri);
+    else gemm_tile<KR, THIN>(g2, b - n1, n2, lds, &ri);
   } else {
     if constexpr (KW >= 0) {
       __shared__ int next_s;
-      __shared__ int offs_s[kMaxExperts + 1];
       gemm_wgrad_tiles<KW>(g3, lds, &next_s, offs_s);
     }
   }
@@ -1470,15 +1560,19 @@ int launch_gemm(const GemmArgs& g, int R, hipStream_t s, const char* name) {
 // Sizes the padded logical tile space of a pipelined launch: MTp row tiles x
 // NTp column tiles (x E for wgrad), whole GM x GN groups.  Returns the number
 // of blocks (0: nothing to do).
+// Row-grouped kinds bound their full row tiles by sum_e ceil(S_e / BM) <=
+// ceil(R / BM) + E; with thin tiles (g.thin) every full tile covers more than
+// THIN rows, so there are at most R / (THIN + 1).
 template <int KIND>
 int64_t pipe_grid(GemmArgs& g, int R) {
   using KT = KindTraits<KIND>;
   constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
-  const int mt = KT::WGRAD ? (g.Mdim + pipe::BM - 1) / pipe::BM : (R + pipe::BM - 1) / pipe::BM + g.E;
+  const int mt = KT::WGRAD ? (g.Mdim + pipe::BM - 1) / pipe::BM
+                           : (g.thin ? R / (pipe::THIN + 1) : (R + pipe::BM - 1) / pipe::BM + g.E);
   const int nt = (g.Ndim + BNH - 1) / BNH;
-  if (mt == 0 || nt == 0) return 0;
   g.tiles_m = pipe::round_up(mt, pipe::GM);
   g.tiles_n = pipe::round_up(nt, pipe::GN);
+  if (mt == 0 || nt == 0) return 0;
   return (int64_t)(KT::WGRAD ? g.E : 1) * g.tiles_m * g.tiles_n;
 }
 
@@ -1499,10 +1593,12 @@ int64_t wgrad_blocks(GemmArgs& g, int R) {
 template <int KIND>
 int64_t pipe_grid_thin(GemmArgs& g, int R) {
   static_assert(!KindTraits<KIND>::WGRAD, "row-grouped kinds");
-  if (pipe_grid<KIND>(g, R) == 0) return 0;
-  g.tiles_m = pipe::round_up(g.E, pipe::GM);
+  pipe_grid<KIND>(g, R);  // sizes tiles_n
+  const int mt = std::min(g.E, R);  // at most one thin tile per expert with rows
+  if (mt == 0 || g.tiles_n == 0) return 0;
+  g.tiles_m = pipe::round_up(mt, pipe::GM);
   g.split_parts = 0;  // thin tiles always run whole
-  return pipe::round_up(g.E * g.tiles_n, 8);
+  return pipe::round_up(mt * g.tiles_n, 8);
 }
 
 // One launch of a row-grouped kind KR (full tiles from g1, whose split-tail
