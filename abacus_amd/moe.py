@@ -16,6 +16,7 @@ import dataclasses
 
 import torch
 import torch.distributed as dist
+import torch.nn.functional as F
 
 from abacus_amd import _lib
 from abacus_amd._lib import call, ptr, query
@@ -369,10 +370,23 @@ class MoE(torch.nn.Module):
         record: dict = {}
         speed = router.bias_update_speed if router.training else None
         operands = (x_TD, router.w_DE, _contig(self.w_gate_EDM), _contig(self.w_up_EDM), _contig(self.w_down_EMD))
+        D, M = self.dim, self.w_gate_EDM.shape[2]
+        vec = 16 // x_TD.element_size()  # the GPU kernels move rows in 16-byte vectors
+        Dp, Mp = -(-D // vec) * vec, -(-M // vec) * vec
+        padded = x_TD.is_cuda and (Dp != D or Mp != M)
+        if padded:
+            # D and M zero-padded to whole vectors: zero columns of x and rows of w_DE add exact
+            # zeros to the logits; a zero hidden unit has silu(0) * 0 = 0 and meets a zero row of
+            # w_down; F.pad's backward slices the gradients back to the parameters' shapes.
+            x_p, w_DE, w_gate, w_up, w_down = operands
+            operands = (F.pad(x_p, (0, Dp - D)), F.pad(w_DE, (0, 0, 0, Dp - D)), F.pad(w_gate, (0, Mp - M, 0, Dp - D)),
+                        F.pad(w_up, (0, Mp - M, 0, Dp - D)), F.pad(w_down, (0, Dp - D, 0, Mp - M)))
         need_grad = torch.is_grad_enabled() and any(t.requires_grad for t in operands)
         out_TD = _MoEFunction.apply(
             *operands, router.expert_bias_E, self.top_k, router.route_scale, speed, need_grad, record,
         )
+        if padded:
+            out_TD = out_TD[:, :D]
         router.last_routing = record["routing"]
         return out_TD.reshape(*batch_shape, self.dim)  # (B, L, D)
 

@@ -265,6 +265,37 @@ def test_wide_expert_counts(T, D, M, E, K, dtype):
     check_against(moe, x, target, torch.device("cpu"))
 
 
+@pytest.mark.parametrize("T,D,M,E,K,dtype", [
+    (37, 20, 36, 5, 2, torch.bfloat16),
+    (64, 6, 10, 4, 2, torch.float32),
+    (50, 4, 4, 3, 1, torch.bfloat16),
+    (300, 130, 200, 8, 2, torch.bfloat16),
+], ids=["D20_M36_bf16", "D6_M10_f32", "D4_M4_bf16", "D130_M200_bf16"])
+def test_dims_off_the_vector_width(T, D, M, E, K, dtype):
+    """D or M not a multiple of the kernels' 16-byte vectors (8 bf16, 4 fp32): the layer zero-pads
+    them for the GPU kernels, as the reference takes any dim (moe.py:25-57); forward and backward
+    against the oracle, routing bit-exact on the kernel's logits, gradients in the parameters'
+    shapes."""
+    print(f"\n[moe-pad] T={T} D={D} M={M} E={E} K={K} {dtype}", flush=True)
+    torch.manual_seed(T + D + M)
+    moe = MoE(dim=D, n_experts=E, top_k=K, hidden_dim=M).to(dtype).to(DEV)
+    x = torch.randn(1, T, D, device=DEV).to(dtype)
+    target = torch.randn(1, T, D, device=DEV).to(dtype)
+    moe.train()
+    bias0 = moe.router.expert_bias_E.detach().clone()
+    xr = x.clone().requires_grad_()
+    out = moe(xr)
+    ((out.float() - target.float()) ** 2).mean().backward()
+    assert out.shape == x.shape and xr.grad.shape == x.shape
+    for n, p in moe.named_parameters():
+        assert p.grad is not None and p.grad.shape == p.shape, n
+    r = moe.router.last_routing
+    w_o, idx_o, _ = oracle.route(r.logits_TE.cpu(), bias0.cpu(), K, moe.router.route_scale)
+    assert torch.equal(r.indices_TK.cpu(), idx_o) and torch.equal(r.weights_TK.cpu(), w_o)
+    moe.router.expert_bias_E.copy_(bias0)
+    check_against(moe, x, target, torch.device("cpu"))
+
+
 def test_two_training_steps_track_bias_updates():
     """Two train-mode iterations (tests/test_moe_ep.py:49-71): outputs, grads and the bias."""
     torch.manual_seed(1)
