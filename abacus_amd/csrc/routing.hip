@@ -89,18 +89,28 @@ __device__ inline uint64_t selection_key(float v, int e) {
 // 16-64 lanes per token run the top-k / renormalise epilogue and bump the
 // block's expert histogram.
 // ---------------------------------------------------------------------------
-template <typename T, int NF>
+// WLDS (bf16, E a multiple of 8): the weight operand comes from w_DE itself.
+// Each wave loads its k-blocks' rows of w_DE (32 x E, zero-padded to EP
+// columns) into a private LDS buffer and reads them back transposed
+// (ds_read_b64_tr_b16), so no transposed copy has to be made first; block 0
+// also writes the transposed rows to wt_out, for the backward.  Otherwise the
+// operand is read from wt, the transposed copy.
+template <typename T, int NF, bool WLDS>
 __global__ __launch_bounds__(256) void router_fwd_kernel(
-    const T* __restrict__ x, const T* __restrict__ wt, const T* __restrict__ bias, int T_, int D, int E, int K,
+    const T* __restrict__ x, const T* __restrict__ wt, const T* __restrict__ w_src, T* __restrict__ wt_out,
+    const T* __restrict__ bias, int T_, int D, int E, int K,
     float route_scale, T* __restrict__ logits, T* __restrict__ weights, int64_t* __restrict__ indices,
     int32_t* __restrict__ idx32, float* __restrict__ score, int32_t* __restrict__ hist) {
   constexpr int VEC = VecTraits<T>::kN;
   constexpr int KB = Mma16<T>::kKB;
   constexpr int EP = NF * 16;
+  static_assert(!WLDS || (sizeof(T) == 2 && KB == 32), "the LDS-transposed operand is bf16, 32 k per k-block");
+  constexpr int WROW = EP * 2;  // bytes of one staged w row
   __shared__ float red[4][kRouteTB][EP];
   __shared__ float s_sc[kRouteTB][EP];
   __shared__ float s_sel[kRouteTB][EP];
   __shared__ int s_cnt[EP];
+  __shared__ __align__(16) char s_w[WLDS ? 4 : 1][WLDS ? 32 * WROW : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -120,6 +130,47 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   // U k-blocks per batch, all their loads in flight before their MFMAs: one
   // k-block at a time left the pass waiting out a memory latency per k-block.
   constexpr int U = NF <= 2 ? 8 : (NF <= 4 ? 4 : (NF <= 8 ? 2 : 1));
+  // WLDS: chunk j of this lane in a k-block = w_DE row c / (EP / 8), 8
+  // columns at 8 (c % (EP / 8)), c = lane + 64 j (32 rows x EP / 8 chunks).
+  auto load_w = [&](int kbu, Vec16* r) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+      const int c = lane + 64 * j, rr = c / (EP / 8), cc = c % (EP / 8);
+      r[j] = (kbu + rr < D && cc * 8 < E) ? ld16(w_src + (int64_t)(kbu + rr) * E + cc * 8) : zero16();
+    }
+  };
+  // WLDS: stage a k-block's chunks in this wave's buffer, read the NF
+  // fragments back transposed (lane: expert 16 f + lane % 16, the 8 k at
+  // kbu + 8 (lane / 16)); block 0 writes them to wt_out.
+  auto stage_w = [&](int kbu, const Vec16* r, Vec16* bf) __attribute__((always_inline)) {
+    char* buf = s_w[WLDS ? wave : 0];
+    // A wave's LDS instructions execute in order, so its writes here cannot
+    // overtake its reads of the previous k-block, nor its reads below these
+    // writes; the empty asm keeps the compiler from reordering them.
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+      const int c = lane + 64 * j, rr = c / (EP / 8), cc = c % (EP / 8);
+      st16(buf + rr * WROW + cc * 16, r[j]);
+    }
+    asm volatile("" ::: "memory");
+    const int grp = lane >> 4, s = lane & 15;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int mn = f * 16 + 4 * (s & 3), k = 8 * grp + (s >> 2);
+      typedef short v4i16_t __attribute__((ext_vector_type(4)));
+      const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4i16_t*)(buf + k * WROW + mn * 2));
+      const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4i16_t*)(buf + (k + 4) * WROW + mn * 2));
+      bf[f].w[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+      bf[f].w[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+      bf[f].w[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+      bf[f].w[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+      if (wt_out != nullptr && blockIdx.x == 0 && kbu + 8 * grp < D)
+        st16(wt_out + (int64_t)(f * 16 + s) * D + kbu + 8 * grp, bf[f]);
+    }
+  };
   int kb0 = wave * KB;
   if (vec_ok) {
     for (; kb0 + (U - 1) * 4 * KB < D; kb0 += U * 4 * KB) {
@@ -129,20 +180,37 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
         const int k = kb0 + u * 4 * KB + kg;
         const bool k_ok = k < D;
         a[u] = (row_ok && k_ok) ? ld16(xrow + k) : zero16();
+        if constexpr (WLDS) {
+          load_w(kb0 + u * 4 * KB, b[u]);
+        } else {
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
-          b[u][f] = k_ok ? ld16(wt + (int64_t)(f * 16 + (lane & 15)) * D + k) : zero16();
+          for (int f = 0; f < NF; ++f)
+            b[u][f] = k_ok ? ld16(wt + (int64_t)(f * 16 + (lane & 15)) * D + k) : zero16();
+        }
       }
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u) {
+        if constexpr (WLDS) {
+          Vec16 bf[NF];
+          stage_w(kb0 + u * 4 * KB, b[u], bf);
 #pragma unroll
-        for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a[u], b[u][f]);
+          for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a[u], bf[f]);
+        } else {
+#pragma unroll
+          for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a[u], b[u][f]);
+        }
+      }
     }
   }
   for (int kb = kb0; kb < D; kb += 4 * KB) {
     const int k = kb + kg;
     Vec16 a, b[NF];
-    if (vec_ok) {
+    if constexpr (WLDS) {  // vec_ok holds on this path
+      a = (row_ok && k < D) ? ld16(xrow + k) : zero16();
+      Vec16 r[NF];
+      load_w(kb, r);
+      stage_w(kb, r, b);
+    } else if (vec_ok) {
       const bool k_ok = k < D;
       a = (row_ok && k_ok) ? ld16(xrow + k) : zero16();
 #pragma unroll
@@ -277,23 +345,32 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
   for (int e = lane; e < kMaxE; e += 64) {
     int p = 0;
     if (e < E)
-      for (int b = b0; b < b1; ++b) p += hv(b, e);
+#pragma unroll 16
+      for (int b = b0; b < b1; ++b) p += hv(b, e);  // 16 loads in flight per lane
     part[q][e] = p;
   }
   __syncthreads();
+  // counts, then their exclusive scan over experts: 4 waves of 64, a wave
+  // scan by lane shuffles plus the earlier waves' totals
+  __shared__ int wtot[kMaxE / 64];
+  int c = 0, incl = 0;
   if (tid < kMaxE) {
-    int c = 0;
     for (int i = 0; i < 16; ++i) c += part[i][tid];
     cnt[tid] = c;
+    incl = tid < E ? c : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    if (lane == 63) wtot[q] = incl;
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int i = 0; i < E; ++i) {
-      off[i] = run;
-      run += cnt[i];
-    }
-    off[E] = run;
+  if (tid < E) {
+    int pre = 0;
+    for (int w = 0; w < q; ++w) pre += wtot[w];
+    off[tid] = pre + incl - c;
+    if (tid == E - 1) off[E] = pre + incl;
   }
   __syncthreads();
   if (tid < E) {
@@ -311,6 +388,7 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
   for (int e = lane; e < E; e += 64) {
     int run = off[e];
     for (int i = 0; i < q; ++i) run += part[i][e];
+#pragma unroll 16
     for (int b = b0; b < b1; ++b) {
       base[(int64_t)b * E + e] = run;
       run += hv(b, e);
@@ -1266,14 +1344,35 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   hipStream_t s = (hipStream_t)stream;
   const int EP = e_pad(E);
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
-  if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
-  else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
-  ABACUS_CHECK_LAUNCH("router weight transpose");
+  // bf16 with whole 16-byte rows of w_DE and x: the router reads w_DE itself
+  // and its block 0 writes the transposed copy (for the backward) as it goes.
+  const bool wlds = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && EP <= 64 && nb > 0;
+  if (!wlds) {
+    if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    ABACUS_CHECK_LAUNCH("router weight transpose");
+  }
   if (nb == 0) return 0;
+  if (wlds) {
+#define ROUTER_LAUNCH_W(NF)                                                                                           \
+  hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true>), dim3(nb), dim3(256), 0, s, (const uint16_t*)x_TD,      \
+                     (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws, (const uint16_t*)bias_E,      \
+                     (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE, (uint16_t*)weights_TK,        \
+                     indices_TK, idx_TK, score_TK, hist)
+    switch (EP / 16) {
+      case 1: ROUTER_LAUNCH_W(1); break;
+      case 2: ROUTER_LAUNCH_W(2); break;
+      case 3: ROUTER_LAUNCH_W(3); break;
+      default: ROUTER_LAUNCH_W(4); break;
+    }
+#undef ROUTER_LAUNCH_W
+    ABACUS_CHECK_LAUNCH("router_fwd");
+    return 0;
+  }
 #define ROUTER_LAUNCH(TT, NF)                                                                                      \
-  hipLaunchKernelGGL((router_fwd_kernel<TT, NF>), dim3(nb), dim3(256), 0, s, (const TT*)x_TD, (const TT*)wt_ws,    \
-                     (const TT*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale, (TT*)logits_TE,             \
-                     (TT*)weights_TK, indices_TK, idx_TK, score_TK, hist)
+  hipLaunchKernelGGL((router_fwd_kernel<TT, NF, false>), dim3(nb), dim3(256), 0, s, (const TT*)x_TD,              \
+                     (const TT*)wt_ws, (const TT*)nullptr, (TT*)nullptr, (const TT*)bias_E, (int)T, (int)D, (int)E, \
+                     (int)K, route_scale, (TT*)logits_TE, (TT*)weights_TK, indices_TK, idx_TK, score_TK, hist)
 #define ROUTER_DISPATCH_NF(TT)          \
   switch (EP / 16) {                    \
     case 1: ROUTER_LAUNCH(TT, 1); break; \

@@ -264,11 +264,15 @@ def main():
     state = {k: v.detach().clone() for k, v in moe.state_dict().items()} if not args.no_cpu_baseline else None
     moe = moe.to(dev)
     x, target = x_cpu.to(dev), target_cpu.to(dev)
-    moe.train()
+    # Training workloads run in train mode (the router's bias step included) with the bias reset
+    # before every step, so every step routes as the first; forward-only workloads are inference
+    # and run in eval mode, where the bias does not move (router.py:53).
+    moe.train(wl.backward)
     bias0 = moe.router.expert_bias_E.detach().clone()
 
     def step():
-        moe.router.expert_bias_E.copy_(bias0)  # every step routes as the first
+        if wl.backward:
+            moe.router.expert_bias_E.copy_(bias0)
         moe.zero_grad(set_to_none=True)
         xi = x.requires_grad_(wl.backward)
         with torch.set_grad_enabled(wl.backward):
@@ -378,7 +382,8 @@ def main():
         "dtype": "bf16" if wl.dtype == torch.bfloat16 else "fp32",
         "data": (f"synthetic, the workload recipe: seed {wl.seed}, module init on the host, N(0,0.02^2) weights, "
                  "N(0,1) activations and target" + (", Zipf(1.2) selection bias" if wl.zipf_bias else "")),
-        "config": {"workload": f"{wl.name}: MoE layer {'fwd+bwd' if wl.backward else 'fwd'}, T={wl.tokens} "
+        "config": {"workload": f"{wl.name}: MoE layer {'fwd+bwd, train mode' if wl.backward else 'fwd, eval mode'}, "
+                               f"T={wl.tokens} "
                                f"(batch {wl.batch} x seq {wl.seq}), "
                                f"D={wl.dim}, E={wl.n_experts}, K={wl.top_k}, M={wl.hidden}",
                    "tokens": wl.tokens, "d_model": wl.dim, "n_experts": wl.n_experts, "top_k": wl.top_k,
