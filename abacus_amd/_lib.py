@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "abacus_moe_route_scan": (_I, [_P, _I64, _I64, _I64, _P, _F, _I, _P, _P, _P, _P]),
     "abacus_moe_permute_gather": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
+    "abacus_moe_dispatch": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _F, _I, _P, _P, _P, _P, _P, _P, _P]),
     "abacus_moe_gateup_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
     "abacus_moe_down_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _P]),
     "abacus_moe_combine_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),

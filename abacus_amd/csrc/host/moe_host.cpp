@@ -493,6 +493,14 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
   return 0;
 }
 
+int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* idx_TK, int64_t T, int64_t D,
+                        int64_t E, int64_t K, void* bias_E, float speed, int dtype, int32_t* counts_E,
+                        int32_t* offsets_E1, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD, int32_t* base_ws,
+                        void* stream) {
+  if (abacus_moe_route_scan(hist, T, E, K, bias_E, speed, dtype, base_ws, counts_E, offsets_E1, stream)) return 1;
+  return abacus_moe_permute_gather(x_TD, idx_TK, base_ws, T, D, E, K, dtype, pos_TK, perm_R, x_perm_RD, stream);
+}
+
 int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const void* w_up_EDM,
                           const int32_t* offsets_E1, int64_t R, int64_t D, int64_t M, int64_t E, int dtype,
                           void* gate_RM, void* up_RM, void* h_RM, void*) {

@@ -408,21 +408,83 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
 // (and loads) in flight when there are few tokens.
 // ---------------------------------------------------------------------------
 constexpr int kPermuteBatch = 8;
+// SCAN: histograms of at most this many ints (nb x E) are scanned by every
+// gather block itself (abacus_moe_dispatch), with no scan launch before it.
+constexpr int kFusedScanInts = 4096;
 
-template <typename T>
+// SCAN (hist holds the router's block histograms; base is unused): each block
+// stages the histograms in LDS and derives the expert counts, offsets and its
+// own block's first rows (the sums route_scan_kernel makes); block (0, 0) also
+// writes counts and offsets and applies the bias step (bias non-NULL).
+template <typename T, bool SCAN>
 __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict__ x, const int32_t* __restrict__ idx,
                                                              const int32_t* __restrict__ base, int T_, int D, int E,
                                                              int K, int32_t* __restrict__ pos,
-                                                             int32_t* __restrict__ perm, T* __restrict__ xp) {
+                                                             int32_t* __restrict__ perm, T* __restrict__ xp,
+                                                             const int32_t* __restrict__ hist,
+                                                             T* __restrict__ bias, float speed,
+                                                             int32_t* __restrict__ counts,
+                                                             int32_t* __restrict__ offsets) {
   constexpr int VEC = VecTraits<T>::kN;
   constexpr int U = kPermuteBatch;
   static_assert(kRouteTB * kMaxK <= 256, "one thread per (token, slot) pair");
+  static_assert(kMaxE == 256, "one thread per expert in the scan");
   __shared__ int s_e[kRouteTB][kMaxK];
   __shared__ int s_pos[kRouteTB][kMaxK];
+  __shared__ int s_h[SCAN ? kFusedScanInts : 1];
+  __shared__ int s_all[SCAN ? 4 : 1][kMaxE], s_prev[SCAN ? 4 : 1][kMaxE], s_base[SCAN ? kMaxE : 1];
+  __shared__ int s_wtot[4];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * kRouteTB;
   const bool writer = blockIdx.y == 0;
   const int ntok = min(kRouteTB, T_ - t0);
+  if constexpr (SCAN) {
+    const int nb = (int)gridDim.x, lane = tid & 63, q = tid >> 6;
+    for (int i = tid; i < nb * E; i += 256) s_h[i] = hist[i];
+    __syncthreads();
+    // wave q: blocks b0 .. b1-1, experts lane, lane + 64, ...; all of them and those before this block
+    const int per = (nb + 3) / 4, b0 = q * per, b1 = min(nb, b0 + per);
+    for (int e = lane; e < kMaxE; e += 64) {
+      int all = 0, prev = 0;
+      if (e < E)
+        for (int b = b0; b < b1; ++b) {
+          const int h = s_h[b * E + e];
+          all += h;
+          prev += b < (int)blockIdx.x ? h : 0;
+        }
+      s_all[q][e] = all;
+      s_prev[q][e] = prev;
+    }
+    __syncthreads();
+    // thread e: count of expert e; exclusive scan over experts by wave shuffles
+    const int e = tid;
+    const int c = ((s_all[0][e] + s_all[1][e]) + s_all[2][e]) + s_all[3][e];
+    int incl = c;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_wtot[q] = incl;
+    __syncthreads();
+    int pre = 0;
+    for (int w = 0; w < q; ++w) pre += s_wtot[w];
+    const int off = pre + incl - c;
+    if (e < E) {
+      s_base[e] = off + ((s_prev[0][e] + s_prev[1][e]) + s_prev[2][e]) + s_prev[3][e];
+      if (blockIdx.x == 0 && blockIdx.y == 0) {
+        counts[e] = c;
+        offsets[e] = off;
+        if (e == E - 1) offsets[E] = off + c;
+        if (bias != nullptr) {  // as route_scan_kernel (router.py:68)
+          const int64_t violation = (int64_t)T_ * K - (int64_t)c * E;
+          const float step = violation > 0 ? 1.0f : (violation < 0 ? -1.0f : 0.0f);
+          bias[e] = from_f32<T>(to_f32<T>(bias[e]) + round_to<T>(speed * step));
+        }
+      }
+    }
+    __syncthreads();
+  }
   if (tid < kRouteTB * K) {
     const int tok = tid / K, k = tid % K;
     s_e[tok][k] = tok < ntok ? idx[(int64_t)(t0 + tok) * K + k] : -1;
@@ -434,7 +496,7 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     int rank = 0;
     for (int t2 = 0; t2 < tok; ++t2)
       for (int k2 = 0; k2 < K; ++k2) rank += s_e[t2][k2] == e ? 1 : 0;
-    const int p = base[(int64_t)blockIdx.x * E + e] + rank;
+    const int p = (SCAN ? s_base[e] : base[(int64_t)blockIdx.x * E + e]) + rank;
     if (writer) {
       pos[(int64_t)(t0 + tok) * K + k] = p;
       perm[p] = t0 + tok;
@@ -1430,12 +1492,44 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
   const unsigned ysplit = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nvec / 64, (1024 + nb - 1) / nb));
   const dim3 grid((unsigned)nb, ysplit);
   if (dtype == kBF16)
-    hipLaunchKernelGGL(permute_gather_kernel<uint16_t>, grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
-                       base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD);
+    hipLaunchKernelGGL((permute_gather_kernel<uint16_t, false>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
+                       base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, nullptr, nullptr,
+                       0.f, nullptr, nullptr);
   else
-    hipLaunchKernelGGL(permute_gather_kernel<float>, grid, dim3(256), 0, s, (const float*)x_TD, idx_TK, base,
-                       (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD);
+    hipLaunchKernelGGL((permute_gather_kernel<float, false>), grid, dim3(256), 0, s, (const float*)x_TD, idx_TK, base,
+                       (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD, nullptr, nullptr, 0.f,
+                       nullptr, nullptr);
   ABACUS_CHECK_LAUNCH("permute_gather");
+  return 0;
+}
+
+int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* idx_TK, int64_t T, int64_t D,
+                        int64_t E, int64_t K, void* bias_E, float bias_update_speed, int dtype, int32_t* counts_E,
+                        int32_t* offsets_E1, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD, int32_t* base_ws,
+                        void* stream) {
+  if (check_route_shape(T, D, E, K, dtype)) return 1;
+  const int64_t nb = (T + kRouteTB - 1) / kRouteTB;
+  if (nb * E > kFusedScanInts) {  // the scan as its own launch, then the gather
+    if (abacus_moe_route_scan(hist, T, E, K, bias_E, bias_update_speed, dtype, base_ws, counts_E, offsets_E1, stream))
+      return 1;
+    return abacus_moe_permute_gather(x_TD, idx_TK, base_ws, T, D, E, K, dtype, pos_TK, perm_R, x_perm_RD, stream);
+  }
+  if (nb == 0)  // no gather blocks: the scan writes the zero counts and offsets (and the bias step)
+    return abacus_moe_route_scan(hist, T, E, K, bias_E, bias_update_speed, dtype, base_ws, counts_E, offsets_E1,
+                                 stream);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t nvec = D / vec_elems(dtype);
+  const unsigned ysplit = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nvec / 64, (1024 + nb - 1) / nb));
+  const dim3 grid((unsigned)nb, ysplit);
+  if (dtype == kBF16)
+    hipLaunchKernelGGL((permute_gather_kernel<uint16_t, true>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
+                       nullptr, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, hist,
+                       (uint16_t*)bias_E, bias_update_speed, counts_E, offsets_E1);
+  else
+    hipLaunchKernelGGL((permute_gather_kernel<float, true>), grid, dim3(256), 0, s, (const float*)x_TD, idx_TK,
+                       nullptr, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD, hist,
+                       (float*)bias_E, bias_update_speed, counts_E, offsets_E1);
+  ABACUS_CHECK_LAUNCH("dispatch");
   return 0;
 }
 

@@ -150,14 +150,14 @@ class _MoEFunction(torch.autograd.Function):
         counts = torch.empty(E, dtype=torch.int32, device=dev)
         offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
         update = bias_speed is not None and bias_speed != 0
-        call(
-            "abacus_moe_route_scan", ptr(hist), T, E, K, ptr(bias_E) if update else None,
-            float(bias_speed) if update else 0.0, dt, ptr(base), ptr(counts), ptr(offsets), s,
-        )
         pos = torch.empty(T, K, dtype=torch.int32, device=dev)
         perm = torch.empty(R, dtype=torch.int32, device=dev)
         xp = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
-        call("abacus_moe_permute_gather", ptr(x_TD), ptr(idx32), ptr(base), T, D, E, K, dt, ptr(pos), ptr(perm), ptr(xp), s)
+        call(
+            "abacus_moe_dispatch", ptr(hist), ptr(x_TD), ptr(idx32), T, D, E, K, ptr(bias_E) if update else None,
+            float(bias_speed) if update else 0.0, dt, ptr(counts), ptr(offsets), ptr(pos), ptr(perm), ptr(xp),
+            ptr(base), s,
+        )
         gate = torch.empty(R, M, dtype=x_TD.dtype, device=dev) if need_grad else None
         up = torch.empty(R, M, dtype=x_TD.dtype, device=dev) if need_grad else None
         h = torch.empty(R, M, dtype=x_TD.dtype, device=dev)

@@ -82,6 +82,17 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
                               int64_t E, int64_t K, int dtype, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD,
                               void* stream);
 
+/* Replaces moe.py:72-77 (the per-expert counting, the optional bias step of
+ * router.py:57-70, and the gather) in one call: abacus_moe_route_scan then
+ * abacus_moe_permute_gather, with the same outputs.  When the router's block
+ * histograms hold at most 4096 ints (ceil(T / 16) * E) the gather blocks
+ * scan them themselves and there is one launch; base_ws (hist-length ints)
+ * is then unused. */
+int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* idx_TK, int64_t T, int64_t D,
+                        int64_t E, int64_t K, void* bias_E, float bias_update_speed, int dtype, int32_t* counts_E,
+                        int32_t* offsets_E1, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD, int32_t* base_ws,
+                        void* stream);
+
 /* Replaces moe.py:78-79 for every expert: gate = x @ w_gate[e],
  * up = x @ w_up[e], h = silu(gate) * up.  gate_RM / up_RM may be NULL
  * (inference: only h is written). */

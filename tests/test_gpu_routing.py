@@ -136,3 +136,55 @@ def test_selection_order_special_values(E, K, dtype):
     """NaN, +-inf, exact ties and zero selections: see tests/special_selection.py."""
     print(f"\n[routing-special] E={E} K={K} {dtype}", flush=True)
     check_special_selection(E, K, dtype, DEV)
+
+
+@pytest.mark.parametrize("T,D,E,K,dtype", [(1, 64, 4, 2, torch.float32), (200, 128, 64, 6, torch.bfloat16),
+                                           (4096, 256, 8, 2, torch.bfloat16), (3000, 64, 16, 4, torch.float32),
+                                           (5000, 64, 16, 2, torch.bfloat16), (33, 72, 256, 16, torch.bfloat16)])
+def test_dispatch_matches_scan_then_gather(T, D, E, K, dtype):
+    """abacus_moe_dispatch (one launch when the block histograms hold at most 4096 ints: the gather
+    blocks scan them) equals abacus_moe_route_scan + abacus_moe_permute_gather bit for bit:
+    counts, offsets, pos, perm, the gathered rows and the bias step."""
+    from abacus_amd._lib import call, ptr, query, stream_of, dtype_code
+    print(f"\n[dispatch] T={T} D={D} E={E} K={K} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(T + E)
+    router = Router(D, E, K).to(device=DEV, dtype=dtype)
+    x = torch.randn(T, D, generator=gen).to(device=DEV, dtype=dtype)
+    router.eval()
+    with torch.no_grad():
+        router(x)
+    r = router.last_routing
+    idx = r.indices_TK.to(torch.int32).contiguous()
+    # the block histograms as the router kernel writes them: counts per 16-token block
+    nb = (T + 15) // 16
+    hist = torch.zeros(nb, E, dtype=torch.int32)
+    for t, row in enumerate(idx.cpu().tolist()):
+        for e in row:
+            hist[t // 16, e] += 1
+    hist = hist.to(DEV).reshape(-1).contiguous()
+    assert hist.numel() == query("abacus_moe_hist_len", T, E)
+    dt, s = dtype_code(dtype), stream_of(DEV)
+    bias0 = (torch.randn(E, generator=gen) * 0.1).to(device=DEV, dtype=dtype)
+    outs = []
+    for fused in (False, True):
+        bias = bias0.clone()
+        counts = torch.full((E,), -1, dtype=torch.int32, device=DEV)
+        offsets = torch.full((E + 1,), -1, dtype=torch.int32, device=DEV)
+        pos = torch.full((T, K), -1, dtype=torch.int32, device=DEV)
+        perm = torch.full((T * K,), -1, dtype=torch.int32, device=DEV)
+        xp = torch.full((T * K, D), float("nan"), dtype=dtype, device=DEV)
+        base = torch.full_like(hist, -1)
+        if fused:
+            call("abacus_moe_dispatch", ptr(hist), ptr(x), ptr(idx), T, D, E, K, ptr(bias), 0.25, dt, ptr(counts),
+                 ptr(offsets), ptr(pos), ptr(perm), ptr(xp), ptr(base), s)
+        else:
+            call("abacus_moe_route_scan", ptr(hist), T, E, K, ptr(bias), 0.25, dt, ptr(base), ptr(counts),
+                 ptr(offsets), s)
+            call("abacus_moe_permute_gather", ptr(x), ptr(idx), ptr(base), T, D, E, K, dt, ptr(pos), ptr(perm),
+                 ptr(xp), s)
+        torch.cuda.synchronize()
+        outs.append((counts.cpu(), offsets.cpu(), pos.cpu(), perm.cpu(), xp.cpu(), bias.cpu()))
+    for name, a, b in zip(("counts", "offsets", "pos", "perm", "xp", "bias"), *outs):
+        assert torch.equal(a, b), name
+    counts_o, offsets_o, perm_o, pos_o = oracle.dispatch(idx.cpu().long(), E)
+    assert outs[1][0].tolist() == counts_o.tolist() and outs[1][3].tolist() == perm_o.tolist()
