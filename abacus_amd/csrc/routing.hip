@@ -432,7 +432,7 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
   __shared__ int s_e[kRouteTB][kMaxK];
   __shared__ int s_pos[kRouteTB][kMaxK];
   __shared__ int s_h[SCAN ? kFusedScanInts : 1];
-  __shared__ int s_all[SCAN ? 4 : 1][kMaxE], s_prev[SCAN ? 4 : 1][kMaxE], s_base[SCAN ? kMaxE : 1];
+  __shared__ int s_all[SCAN ? 256 : 1], s_prev[SCAN ? 256 : 1], s_base[SCAN ? kMaxE : 1];
   __shared__ int s_wtot[4];
   const int tid = threadIdx.x;
   const int t0 = blockIdx.x * kRouteTB;
@@ -442,23 +442,29 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     const int nb = (int)gridDim.x, lane = tid & 63, q = tid >> 6;
     for (int i = tid; i < nb * E; i += 256) s_h[i] = hist[i];
     __syncthreads();
-    // wave q: blocks b0 .. b1-1, experts lane, lane + 64, ...; all of them and those before this block
-    const int per = (nb + 3) / 4, b0 = q * per, b1 = min(nb, b0 + per);
-    for (int e = lane; e < kMaxE; e += 64) {
+    // thread t: expert t % E over blocks t / E, t / E + NP, ... (NP = 256 / E parts), all of
+    // them and those before this block; then thread e adds its expert's NP parts
+    const int NP = 256 / E, part = tid / E, ex = tid % E;
+    {
       int all = 0, prev = 0;
-      if (e < E)
-        for (int b = b0; b < b1; ++b) {
-          const int h = s_h[b * E + e];
+      if (part < NP)
+        for (int b = part; b < nb; b += NP) {
+          const int h = s_h[b * E + ex];
           all += h;
           prev += b < (int)blockIdx.x ? h : 0;
         }
-      s_all[q][e] = all;
-      s_prev[q][e] = prev;
+      s_all[tid] = all;
+      s_prev[tid] = prev;
     }
     __syncthreads();
     // thread e: count of expert e; exclusive scan over experts by wave shuffles
     const int e = tid;
-    const int c = ((s_all[0][e] + s_all[1][e]) + s_all[2][e]) + s_all[3][e];
+    int c = 0, prv = 0;
+    if (e < E)
+      for (int i = 0; i < NP; ++i) {
+        c += s_all[i * E + e];
+        prv += s_prev[i * E + e];
+      }
     int incl = c;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -471,7 +477,7 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     for (int w = 0; w < q; ++w) pre += s_wtot[w];
     const int off = pre + incl - c;
     if (e < E) {
-      s_base[e] = off + ((s_prev[0][e] + s_prev[1][e]) + s_prev[2][e]) + s_prev[3][e];
+      s_base[e] = off + prv;
       if (blockIdx.x == 0 && blockIdx.y == 0) {
         counts[e] = c;
         offsets[e] = off;

@@ -66,7 +66,7 @@ def parse_args():
 def hbm_bytes(wl, name):
     """Algorithmic HBM bytes per launch for the memory-bound entry points."""
     s, T, R, D, K = wl.elem_bytes(), wl.tokens, wl.rows, wl.dim, wl.top_k
-    if name == "abacus_moe_permute_gather":
+    if name in ("abacus_moe_permute_gather", "abacus_moe_dispatch"):
         return wl.dispatch_bytes()
     if name == "abacus_moe_combine_fwd":
         return wl.combine_bytes()
