@@ -1533,8 +1533,12 @@ template <int KIND> struct Cfg<uint16_t, KIND> {
   static constexpr int v[7] = {ABACUS_BF16_CFG};
   static constexpr int BM = v[0], BN = v[1], BK = v[2], WM = v[3], WN = v[4], SHAPE = v[5], MINB = v[6];
 };
+#ifndef ABACUS_F32_CFG
+#define ABACUS_F32_CFG 128, 128, 32, 2, 2, 32, 2
+#endif
 template <int KIND> struct Cfg<float, KIND> {
-  static constexpr int BM = 128, BN = 128, BK = 32, WM = 2, WN = 2, SHAPE = 16, MINB = 2;
+  static constexpr int v[7] = {ABACUS_F32_CFG};
+  static constexpr int BM = v[0], BN = v[1], BK = v[2], WM = v[3], WN = v[4], SHAPE = v[5], MINB = v[6];
 };
 
 template <typename T, int KIND>
