@@ -549,6 +549,16 @@ __device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
 // of one bank period get distinct chunk permutations.
 __device__ inline int kc_off(int row, int chunk) { return (row * CPR + (chunk ^ ((row / (16 / CPR)) % CPR))) * 16; }
 __device__ inline int mc_off(int k, int chunk) { return (k * 32 + (chunk ^ ((k & 3) << 2))) * 16; }
+// The mn-contiguous tile of fp32 operands: [32 k][64 chunks] (the same 32 KB),
+// chunks XOR-swizzled by groups of 8 per 4 k rows so that the two half-waves
+// of a fragment read (rows k and k + 4) hit different banks.
+__device__ inline int mc_off32(int k, int chunk) { return (k * 64 + (chunk ^ (((k >> 2) & 7) << 3))) * 16; }
+template <typename T> __device__ inline int mc_swz(int k);
+template <> __device__ inline int mc_swz<uint16_t>(int k) { return (k & 3) << 2; }
+template <> __device__ inline int mc_swz<float>(int k) { return ((k >> 2) & 7) << 3; }
+// k-tile depth in elements: 128 bytes of k per row for either dtype
+template <typename T> constexpr int kBKT = 128 / (int)sizeof(T);
+static_assert(kBKT<uint16_t> == BK, "the bf16 k-tile");
 
 
 // 1 / (1 + exp(-x)) from the hardware exp2 and reciprocal (a few ulp in fp32,
@@ -565,14 +575,15 @@ __device__ inline float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.0f 
 // source pointers once and issue() adds the k0 step (kc: k0 elements, mc:
 // k0 rows) -- one 64-bit add per DMA.  Chunks whose k lies beyond k_lim
 // (a ragged segment's tail) read the zero page instead.
-template <bool MC, int N = DMA_PER_OPERAND>
+template <typename T, bool MC, int N = DMA_PER_OPERAND>
 struct DmaStream {
-  const uint16_t* base[N];
+  static constexpr int EPC = 16 / (int)sizeof(T);       // elements per 16-byte chunk
+  static constexpr int MCC = BN * (int)sizeof(T) / 16;  // chunks per mn-contiguous k row
+  const T* base[N];
   int koff[N];   // k of the chunk relative to k0
   int64_t ld;
 
-  __device__ inline void setup(const uint16_t* b0, const uint16_t* b1, int64_t ld_, int r0, int r_lim, int wave,
-                               int lane) {
+  __device__ inline void setup(const T* b0, const T* b1, int64_t ld_, int r0, int r_lim, int wave, int lane) {
     ld = ld_;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
@@ -582,19 +593,19 @@ struct DmaStream {
         const int c = (p % CPR) ^ ((row / (16 / CPR)) % CPR);
         int gr = r0 + row;
         gr = gr < r_lim ? gr : r_lim - 1;
-        base[i] = b0 + (int64_t)gr * ld + c * 8;
-        koff[i] = c * 8;
+        base[i] = b0 + (int64_t)gr * ld + c * EPC;
+        koff[i] = c * EPC;
       } else {
-        const int k = p >> 5;
-        const int c = (p & 31) ^ ((k & 3) << 2);
-        int mn = c * 8;
-        const uint16_t* b = b0;
+        const int k = p / MCC;
+        const int c = (p % MCC) ^ mc_swz<T>(k);
+        int mn = c * EPC;
+        const T* b = b0;
         if (b1 != nullptr && mn >= BN / 2) {
           b = b1;
           mn -= BN / 2;
         }
         int gm = r0 + mn;
-        gm = gm < r_lim ? gm : r_lim - 8;
+        gm = gm < r_lim ? gm : r_lim - EPC;
         base[i] = b + (int64_t)k * ld + gm;
         koff[i] = k;
       }
@@ -616,7 +627,17 @@ __device__ inline Vec16 frag_kc(const char* tile, int f0, int t, int lane) {
   const int r = f0 + (lane & 31);
   return *reinterpret_cast<const Vec16*>(tile + kc_off(r, 2 * t + (lane >> 5)));
 }
-__device__ inline Vec16 frag_mc(const char* tile, int f0, int t, int lane) {
+template <typename T> __device__ inline Vec16 frag_mc(const char* tile, int f0, int t, int lane);
+// fp32: lane l gets the 4 k at 8 t + 4 (l / 32) of column f0 + l % 32 (one
+// 32-bit read each; the MFMA's k order, as frag_kc's 16-byte chunk)
+template <> __device__ inline Vec16 frag_mc<float>(const char* tile, int f0, int t, int lane) {
+  const int cc = f0 + (lane & 31), k0 = 8 * t + 4 * (lane >> 5);
+  Vec16 v;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v.w[j] = *reinterpret_cast<const uint32_t*>(tile + mc_off32(k0 + j, cc >> 2) + (cc & 3) * 4);
+  return v;
+}
+template <> __device__ inline Vec16 frag_mc<uint16_t>(const char* tile, int f0, int t, int lane) {
   const int grp = lane >> 4, s = lane & 15;
   const int mn = f0 + 16 * (grp & 1) + 4 * (s & 3);
   const int k = 16 * t + 8 * (grp >> 1) + (s >> 2);
@@ -844,11 +865,12 @@ __device__ inline TileId tile_of_logical(int L, int MTp, int NTp) {
 // row tiles of row-grouped kinds): block b of the kind's G blocks (G a
 // multiple of 8, so b % 8 is still the XCD the block runs on when a launch
 // runs several kinds back to back).  lds: the work-group's LDS_BYTES.
-template <int KIND, int BMT = BM>
+template <typename T, int KIND, int BMT = BM>
 __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& g, int b, int G, char* lds,
                                                                 const RowIndex* ri) {
   using KT = KindTraits<KIND>;
-  using Op = MfmaOp<uint16_t, 32>;
+  using Op = MfmaOp<T, 32>;
+  constexpr int BKT = kBKT<T>;  // k-tile depth in elements
   using GE = Geo<BMT>;
   static_assert(!KT::WGRAD || BMT == BM, "weight gradients have full tiles only");
   constexpr int FM = GE::FM, WTM = GE::WTM, STAGE_BYTES = GE::STAGE, A_BYTES = GE::A_BYTES;
@@ -890,17 +912,16 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   }
   const int seg0 = KT::WGRAD ? g.offsets[e] : 0;
 
-  const uint16_t* A0 = (const uint16_t*)g.a0;
-  const uint16_t* A1 = (const uint16_t*)g.a1;
-  const uint16_t* B0 = (const uint16_t*)g.b0 + (KT::WGRAD ? 0 : (int64_t)e * g.b_estride);
-  const uint16_t* B1 = KT::DUAL_B || KT::DUAL_K ? (const uint16_t*)g.b1 + (KT::WGRAD ? 0 : (int64_t)e * g.b_estride)
-                                                : nullptr;
+  const T* A0 = (const T*)g.a0;
+  const T* A1 = (const T*)g.a1;
+  const T* B0 = (const T*)g.b0 + (KT::WGRAD ? 0 : (int64_t)e * g.b_estride);
+  const T* B1 = KT::DUAL_B || KT::DUAL_K ? (const T*)g.b1 + (KT::WGRAD ? 0 : (int64_t)e * g.b_estride) : nullptr;
   if (KT::WGRAD) {
     A0 += (int64_t)seg0 * g.lda;
     B0 += (int64_t)seg0 * g.ldb;
     if (KT::DUAL_B) B1 += (int64_t)seg0 * g.ldb;
   }
-  const int ktiles_half = (k_len + BK - 1) / BK;
+  const int ktiles_half = (k_len + BKT - 1) / BKT;
   const int ktiles_all = KT::DUAL_K ? 2 * ktiles_half : ktiles_half;
   // a slice of a split tile runs k-tiles kbase .. kbase + ktiles - 1
   int kbase = 0, ktiles = ktiles_all;
@@ -914,8 +935,8 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 
   // wave index as a scalar so the DMA destinations are computed in SGPRs
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  DmaStream<KT::A_MC, DMA_A> sa;
-  DmaStream<KT::B_NC> sb;
+  DmaStream<T, KT::A_MC, DMA_A> sa;
+  DmaStream<T, KT::B_NC> sb;
   int half_set = 0;
   sa.setup(A0, nullptr, g.lda, row0, a_lim, wave, lane);
   sb.setup(B0, KT::DUAL_B ? B1 : nullptr, g.ldb, n0, g.Ndim, wave, lane);
@@ -933,14 +954,14 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
       sb.setup(B1, nullptr, g.ldb, n0, g.Ndim, wave, lane);
       half_set = half;
     }
-    dma_k0 = (kt - half * ktiles_half) * BK;
+    dma_k0 = (kt - half * ktiles_half) * BKT;
   };
   auto dma = [&](int n) __attribute__((always_inline)) {
     if (n < DMA_A) sa.template issue_one<KT::WGRAD>(n, dma_stage, wave_u, dma_k0, k_len);
     else sb.template issue_one<KT::WGRAD>(n - DMA_A, dma_stage + A_BYTES, wave_u, dma_k0, k_len);
   };
 
-  Op::Acc acc[FM][FN];
+  typename Op::Acc acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -968,10 +989,10 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     const char* Bt = st + A_BYTES;
     if (f == 0 || f > FN) {
       const int i = f == 0 ? 0 : f - FN;
-      af[slot][i] = KT::A_MC ? frag_mc(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
+      af[slot][i] = KT::A_MC ? frag_mc<T>(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
     } else {
       const int j = f - 1;
-      bfr[slot][j] = KT::B_NC ? frag_mc(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
+      bfr[slot][j] = KT::B_NC ? frag_mc<T>(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
     }
   };
 
@@ -1070,6 +1091,60 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
               make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2], acc[i][j][4 * gq + 3]);
     return;
   }
+  if constexpr (sizeof(T) == 4) {
+    // fp32: straight from the accumulators (a 256 x 256 fp32 C tile does not
+    // fit in LDS, and the main loop is long enough that the scattered 16-byte
+    // stores cost little).  Fragment (i, j) holds C^T: lane l has row l % 32
+    // and, for gq = 0..3, columns 8 gq + 4 (l / 32) .. +3.  Same elementwise
+    // epilogues as the generic kernel's fp32 path.
+    const int rl = lane & 31, ch = 4 * (lane >> 5);
+    const int rlim = KT::WGRAD ? g.Mdim : row_end;
+    constexpr int JN = KT::DUAL_B ? FN / 2 : FN;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int row = row0 + wm * WTM + i * 32 + rl;
+      if (row >= rlim) continue;
+#pragma unroll
+      for (int j = 0; j < JN; ++j)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int col = n0 + b_col(j) + 8 * gq + ch;  // dual-B: the gate half; fragment j + JN is up
+          if (col >= g.Ndim) continue;
+          const int64_t o = (int64_t)row * g.ldc + col;
+          const float4 c0 = make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                        acc[i][j][4 * gq + 3]);
+          if constexpr (KIND == kGateUpFwd) {
+            const float4 c1 = make_float4(acc[i][j + JN][4 * gq], acc[i][j + JN][4 * gq + 1],
+                                          acc[i][j + JN][4 * gq + 2], acc[i][j + JN][4 * gq + 3]);
+            const float4 h = make_float4(silu_f32(c0.x) * c1.x, silu_f32(c0.y) * c1.y, silu_f32(c0.z) * c1.z,
+                                         silu_f32(c0.w) * c1.w);
+            if (g.c0) *reinterpret_cast<float4*>((float*)g.c0 + o) = c0;
+            if (g.c1) *reinterpret_cast<float4*>((float*)g.c1 + o) = c1;
+            *reinterpret_cast<float4*>((float*)g.c2 + o) = h;
+          } else if constexpr (KIND == kDownDgrad) {
+            const float4 gi = *reinterpret_cast<const float4*>((const float*)g.x0 + o);
+            const float4 ui = *reinterpret_cast<const float4*>((const float*)g.x1 + o);
+            const float dh[4] = {c0.x, c0.y, c0.z, c0.w}, gv[4] = {gi.x, gi.y, gi.z, gi.w},
+                        uv[4] = {ui.x, ui.y, ui.z, ui.w};
+            float dg[4], du[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float sig = sigmoid_f32(gv[t]);
+              const float act = silu_f32(gv[t]);
+              const float dact = dh[t] * uv[t];
+              dg[t] = dact * sig * (1.0f + gv[t] * (1.0f - sig));
+              du[t] = dh[t] * act;
+            }
+            *reinterpret_cast<float4*>((float*)g.c0 + o) = make_float4(dg[0], dg[1], dg[2], dg[3]);
+            *reinterpret_cast<float4*>((float*)g.c1 + o) = make_float4(du[0], du[1], du[2], du[3]);
+          } else {
+            static_assert(!KT::WGRAD, "fp32 weight gradients run on the generic kernel");
+            *reinterpret_cast<float4*>((float*)g.c0 + o) = c0;
+          }
+        }
+    }
+    return;
+  } else {
   __syncthreads();  // all fragment reads done before the C tile overwrites the stages
 
   // ---------------- epilogue (same contract as the generic kernel) ----------------
@@ -1175,6 +1250,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
       }
     }
   }
+}  // bf16 epilogue
 }
 
 // ---------------- weight gradients: a persistent tile loop ----------------
@@ -1277,8 +1353,8 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
   };
 
   int e = 0, row0 = 0, n0 = 0, k_len = 0, ktiles = 0;
-  DmaStream<true, DMA_A> sa;
-  DmaStream<true> sb;
+  DmaStream<uint16_t, true, DMA_A> sa;
+  DmaStream<uint16_t, true> sb;
   char* dma_stage = lds;
   int dma_k0 = 0;
   auto prep = [&](int kt) __attribute__((always_inline)) {
@@ -1323,10 +1399,10 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
   auto read_frag = [&](const char* st, int t, int slot, int f) __attribute__((always_inline)) {
     if (f == 0 || f > FN) {
       const int i = f == 0 ? 0 : f - FN;
-      af[slot][i] = frag_mc(st, wm * WTM + i * 32, t, lane);
+      af[slot][i] = frag_mc<uint16_t>(st, wm * WTM + i * 32, t, lane);
     } else {
       const int j = f - 1;
-      bfr[slot][j] = frag_mc(st + A_BYTES, b_col(j), t, lane);
+      bfr[slot][j] = frag_mc<uint16_t>(st + A_BYTES, b_col(j), t, lane);
     }
   };
   // The k-step and k-tile schedule of gemm_tile, repeated: sharing one helper
@@ -1456,17 +1532,17 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_wgrad_kernel(GemmArgs g) {
 // (gemm_wgrad_tiles).  Blocks are dispatched in index order, so the long
 // tiles go first and the weight gradient's blocks start on the CUs that the
 // long tiles' last partial round leaves idle.
-template <int KR, int KW>
-__global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, GemmArgs g2, GemmArgs g3, int n1,
-                                                               int n2) {
+template <typename T, int KR, int KW>
+__global__ __launch_bounds__(NT, 1) void gemm_rows_kernel(GemmArgs g1, GemmArgs g2, GemmArgs g3, int n1, int n2) {
+  static_assert(KW < 0 || sizeof(T) == 2, "weight gradients in a row launch: bf16 only");
   __shared__ __attribute__((aligned(1024))) char lds[LDS_ALLOC];
   __shared__ int offs_s[kMaxExperts + 1];
   const int b = blockIdx.x;
   if (b < n1 + n2) {
     __shared__ int cum_s[2][kMaxExperts + 1];
     const RowIndex ri = build_row_index<NT>(g1, offs_s, cum_s[0], cum_s[1]);
-    if (b < n1) gemm_tile<KR, BM>(g1, b, n1, lds, &ri);
-    else gemm_tile<KR, THIN>(g2, b - n1, n2, lds, &ri);
+    if (b < n1) gemm_tile<T, KR, BM>(g1, b, n1, lds, &ri);
+    else gemm_tile<T, KR, THIN>(g2, b - n1, n2, lds, &ri);
   } else {
     if constexpr (KW >= 0) {
       __shared__ int next_s;
@@ -1476,11 +1552,11 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_rows_kernel(GemmArgs g1, Gemm
 }
 
 // Adds the slices of each split tail tile in slice order and writes the tile
-// (kinds whose epilogue is a plain store of the bf16-rounded product).  Block
+// (kinds whose epilogue is a plain store of the product, rounded to T).  Block
 // (i, j) serves rows kSplitReduceRows j .. +kSplitReduceRows-1 of tail tile i:
 // the tail is fewer tiles than CUs, and one block per tile left the pass
 // latency-bound on a few CUs.
-template <int KIND>
+template <typename T, int KIND>
 __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
   using KT = KindTraits<KIND>;
   static_assert(!KT::WGRAD && !KT::DUAL_B && KIND != kDownDgrad, "plain-store epilogues only");
@@ -1515,10 +1591,16 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmArgs g) {
         s[0] += lo[p].x; s[1] += lo[p].y; s[2] += lo[p].z; s[3] += lo[p].w;
         s[4] += hi[p].x; s[5] += hi[p].y; s[6] += hi[p].z; s[7] += hi[p].w;
       }
-    Vec16 out;
+    if constexpr (sizeof(T) == 4) {
+      float* c = (float*)g.c0 + (int64_t)row * g.ldc + col;
+      *reinterpret_cast<float4*>(c) = make_float4(s[0], s[1], s[2], s[3]);
+      *reinterpret_cast<float4*>(c + 4) = make_float4(s[4], s[5], s[6], s[7]);
+    } else {
+      Vec16 out;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) out.w[w] = pack_bf16x2(s[2 * w], s[2 * w + 1]);
-    st16((uint16_t*)g.c0 + (int64_t)row * g.ldc + col, out);
+      for (int w = 0; w < 4; ++w) out.w[w] = pack_bf16x2(s[2 * w], s[2 * w + 1]);
+      st16((uint16_t*)g.c0 + (int64_t)row * g.ldc + col, out);
+    }
   }
 }
 
@@ -1608,7 +1690,7 @@ int64_t pipe_grid_thin(GemmArgs& g, int R) {
 // One launch of a row-grouped kind KR (full tiles from g1, whose split-tail
 // fields may be set, then thin tiles) and, when KW >= 0, a weight gradient
 // (gw) after them.
-template <int KR, int KW>
+template <typename T, int KR, int KW>
 int launch_rows(const GemmArgs& g1, int R, const GemmArgs* gw, int64_t n1, bool thin, hipStream_t s,
                 const char* name) {
   GemmArgs ga = g1, gt = g1, gc = gw ? *gw : g1;
@@ -1628,19 +1710,20 @@ int launch_rows(const GemmArgs& g1, int R, const GemmArgs* gw, int64_t n1, bool 
     hipLaunchKernelGGL(pipe::ctr_zero_kernel, dim3(1), dim3(64), 0, s, gc.tile_ctr);
     ABACUS_CHECK_LAUNCH(name);
   }
-  hipLaunchKernelGGL((pipe::gemm_bf16_rows_kernel<KR, KW>), dim3((unsigned)(n1 + n2 + n3)), dim3(pipe::NT), 0, s, ga,
+  hipLaunchKernelGGL((pipe::gemm_rows_kernel<T, KR, KW>), dim3((unsigned)(n1 + n2 + n3)), dim3(pipe::NT), 0, s, ga,
                      gt, gc, (int)n1, (int)n2);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
 }
 
-template <int KIND>
+template <typename T, int KIND>
 int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
   if constexpr (!KindTraits<KIND>::WGRAD) {
     // (the down projection's forward reduces over M: its tiles are long, and
     // thin ones would end the launch on a partial round of them)
-    return launch_rows<KIND, -1>(g, R, nullptr, -1, KIND != kDownFwd, s, name);
+    return launch_rows<T, KIND, -1>(g, R, nullptr, -1, KIND != kDownFwd, s, name);
   } else {
+    static_assert(sizeof(T) == 2, "pipelined weight gradients: bf16");
     GemmArgs ga = g;
     const int64_t blocks = wgrad_blocks<KIND>(ga, R);
     if (blocks == 0) return 0;
@@ -1694,7 +1777,7 @@ SplitPlan plan_split(const GemmArgs& g, int R) {
   return p;
 }
 
-template <int KIND>
+template <typename T, int KIND>
 int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws, hipStream_t s, const char* name) {
   GemmArgs ga = g;
   if (pipe_grid<KIND>(ga, R) == 0) return 0;
@@ -1702,10 +1785,10 @@ int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws
   ga.split_parts = kSplitParts;
   ga.split_cus = cu_count();
   ga.split_ws = ws;
-  if (launch_rows<KIND, -1>(ga, R, nullptr, (int64_t)plan.whole_blocks + plan.slice_blocks, false, s, name))
+  if (launch_rows<T, KIND, -1>(ga, R, nullptr, (int64_t)plan.whole_blocks + plan.slice_blocks, false, s, name))
     return 1;
   ga.thin = 0;
-  hipLaunchKernelGGL(pipe::split_reduce_kernel<KIND>, dim3((unsigned)plan.tail_max, pipe::BM / kSplitReduceRows), dim3(256),
+  hipLaunchKernelGGL((pipe::split_reduce_kernel<T, KIND>), dim3((unsigned)plan.tail_max, pipe::BM / kSplitReduceRows), dim3(256),
                      0, s, ga);
   ABACUS_CHECK_LAUNCH(name);
   return 0;
@@ -1716,22 +1799,35 @@ int launch_pipe_split(const GemmArgs& g, int R, const SplitPlan& plan, float* ws
 template <int KA, int KB>
 int launch_pipe_pair(const GemmArgs& a, int Ra, const GemmArgs& b, int Rb, hipStream_t s, const char* name) {
   (void)Rb;
-  return launch_rows<KA, KB>(a, Ra, &b, -1, true, s, name);
+  return launch_rows<uint16_t, KA, KB>(a, Ra, &b, -1, true, s, name);
 }
 
-// bf16: the pipelined DMA kernel whenever every dimension it tiles is a
-// whole number of 16-byte chunks and the fixed reduction length is a whole
-// number of k-tiles (always true for the workloads; the generic kernel covers
-// the rest).  fp32: the generic kernel.
+// The pipelined DMA kernel whenever every dimension it tiles is a whole
+// number of 16-byte chunks and the fixed reduction length is a whole number
+// of k-tiles (always true for the workloads; the generic kernel covers the
+// rest).  The routed-row count of a row-grouped kind is free: its tiles clamp
+// their row addresses to the expert's last row.  bf16: every kind.  fp32:
+// the gate/up forward and data gradient and the down projection's forward,
+// once the rows fill at least one round of 256 x 256 tiles over the CUs
+// (below that the generic kernel's 128 x 128 tiles reach more CUs); the fp32
+// down-projection data gradient, whose epilogue also reads G and U, and the
+// fp32 weight gradients measured faster on the generic kernel.
 template <int KIND>
-bool pipe_ok(int dtype, const GemmArgs& g) {
-  return dtype == kBF16 && (KindTraits<KIND>::WGRAD || g.Kdim % pipe::BK == 0) && g.Ndim % 8 == 0 &&
-         g.Mdim % 8 == 0;
+bool pipe_ok(int dtype, const GemmArgs& g, int R) {
+  using KT = KindTraits<KIND>;
+  if (g.Ndim % 8 != 0 || (KT::WGRAD && g.Mdim % 8 != 0)) return false;
+  if (dtype == kBF16) return KT::WGRAD || g.Kdim % pipe::BK == 0;
+  if (dtype != kF32 || KT::WGRAD || KIND == kDownDgrad || g.Kdim % pipe::kBKT<float> != 0) return false;
+  constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
+  return (int64_t)((R + pipe::BM - 1) / pipe::BM) * ((g.Ndim + BNH - 1) / BNH) >= cu_count();
 }
 
 template <int KIND>
 int dispatch_gemm(int dtype, const GemmArgs& g, int R, hipStream_t s, const char* name) {
-  if (pipe_ok<KIND>(dtype, g)) return launch_pipe<KIND>(g, R, s, name);
+  if (pipe_ok<KIND>(dtype, g, R)) {
+    if (dtype == kBF16) return launch_pipe<uint16_t, KIND>(g, R, s, name);
+    if constexpr (!KindTraits<KIND>::WGRAD && KIND != kDownDgrad) return launch_pipe<float, KIND>(g, R, s, name);
+  }
   if (dtype == kBF16) return launch_gemm<uint16_t, KIND>(g, R, s, name);
   return launch_gemm<float, KIND>(g, R, s, name);
 }
@@ -1743,7 +1839,8 @@ template <int KD, int KW>
 int dispatch_pair(int dtype, const GemmArgs& gd, const GemmArgs& gw, int R, hipStream_t s, const char* name_d,
                   const char* name_w, const char* name) {
   if (R == 0) return dispatch_gemm<KW>(dtype, gw, R, s, name_w);
-  if (pipe_ok<KD>(dtype, gd) && pipe_ok<KW>(dtype, gw)) return launch_pipe_pair<KD, KW>(gd, R, gw, R, s, name);
+  if (dtype == kBF16 && pipe_ok<KD>(dtype, gd, R) && pipe_ok<KW>(dtype, gw, R))
+    return launch_pipe_pair<KD, KW>(gd, R, gw, R, s, name);
   if (dispatch_gemm<KD>(dtype, gd, R, s, name_d)) return 1;
   return dispatch_gemm<KW>(dtype, gw, R, s, name_w);
 }
@@ -1903,7 +2000,7 @@ static bool down_fwd_thin(int64_t R, int64_t E) { return R <= (int64_t)pipe::THI
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype) {
   if (check_gemm_shape(R, D, M, E, dtype) || R == 0) return 0;
   const GemmArgs g = args_down_fwd(nullptr, nullptr, nullptr, R, M, D, E, nullptr);
-  if (!pipe_ok<kDownFwd>(dtype, g) || down_fwd_thin(R, E)) return 0;  // no split tail: no workspace
+  if (!pipe_ok<kDownFwd>(dtype, g, (int)R) || down_fwd_thin(R, E)) return 0;  // no split tail
   return plan_split<kDownFwd>(g, (int)R).ws_bytes();
 }
 
@@ -1912,13 +2009,17 @@ int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t*
   if (check_gemm_shape(R, D, M, E, dtype)) return 1;
   if (R == 0) return 0;
   const GemmArgs g = args_down_fwd(h_RM, w_down_EMD, offsets_E1, R, M, D, E, y_RD);
-  if (pipe_ok<kDownFwd>(dtype, g)) {
+  if (pipe_ok<kDownFwd>(dtype, g, (int)R)) {
     if (down_fwd_thin(R, E))
-      return launch_rows<kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd");
+      return dtype == kBF16
+                 ? launch_rows<uint16_t, kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd")
+                 : launch_rows<float, kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd");
     if (ws != nullptr) {
       const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);
       if (plan.on() && ws_bytes >= plan.ws_bytes())
-        return launch_pipe_split<kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd");
+        return dtype == kBF16
+                   ? launch_pipe_split<uint16_t, kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd")
+                   : launch_pipe_split<float, kDownFwd>(g, (int)R, plan, (float*)ws, (hipStream_t)stream, "down_fwd");
     }
   }
   return dispatch_gemm<kDownFwd>(dtype, g, (int)R, (hipStream_t)stream, "down_fwd");

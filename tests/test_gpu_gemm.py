@@ -216,6 +216,63 @@ def test_row_tiles_every_remainder_class(counts):
               f"dX expert {e}")
 
 
+def test_fp32_row_products_at_pipelined_sizes():
+    """fp32 row-grouped products with enough rows for the pipelined kernel (at least one round
+    of 256 x 256 tiles per CU on a 256-CU GPU): every remainder class of an expert's last
+    tile, an empty and a one-row expert, the down projection's forward with its split tail
+    and without it, each expert's rows against the fp64 product (relative error 1e-5)."""
+    base = [256, 257, 383, 384, 385, 511, 512, 1, 128, 129, 0, 130]
+    counts = [c + (1536 if c > 1 else 0) for c in base] + [4000, 3000]
+    D, M = 1024, 1024
+    o = _operands(counts, D, M, torch.float32, seed=41)
+    E, R = o["E"], o["R"]
+    assert R >= 256 * 256 // (D // 256)
+    s = _lib.stream_of(torch.device("cuda"))
+    nan = lambda *shape: torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+    G, U, H, Y, Yw = nan(R, M), nan(R, M), nan(R, M), nan(R, D), nan(R, D)
+    dG, dU, dX = nan(R, M), nan(R, M), nan(R, D)
+    ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, E, 0)
+    assert ws_bytes > 0, "this shape has a partial last round on any GPU of up to 256 CUs"
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    call("abacus_moe_gateup_fwd", ptr(o["xp"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["offsets"]), R, D, M, E, 0,
+         ptr(G), ptr(U), ptr(H), s)
+    call("abacus_moe_down_fwd", ptr(o["h"]), ptr(o["w_down"]), ptr(o["offsets"]), R, M, D, E, 0, ptr(Y), ptr(ws),
+         ws_bytes, s)
+    call("abacus_moe_down_fwd", ptr(o["h"]), ptr(o["w_down"]), ptr(o["offsets"]), R, M, D, E, 0, ptr(Yw), None, 0, s)
+    call("abacus_moe_down_bwd_dgrad", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]),
+         ptr(o["offsets"]), R, M, D, E, 0, ptr(dG), ptr(dU), s)
+    call("abacus_moe_gateup_bwd_dgrad", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]),
+         ptr(o["offsets"]), R, D, M, E, 0, ptr(dX), s)
+    torch.cuda.synchronize()
+    for name, t in (("G", G), ("U", U), ("H", H), ("Y", Y), ("Y whole", Yw), ("dG", dG), ("dU", dU), ("dX", dX)):
+        assert not torch.isnan(t).any(), f"{name}: rows left unwritten"
+    f = lambda t: t.double()  # fp64 products on the GPU: the CPU would take minutes at this size
+    off = o["offsets"].tolist()
+
+    def close(got, want, what):
+        err = float((f(got) - want).norm() / max(want.norm().item(), 1e-30))
+        assert err < 1e-5, f"{what}: relative error {err:.3g}"
+
+    for e in range(E):
+        a, b = off[e], off[e + 1]
+        if a == b:
+            continue
+        close(G[a:b], f(o["xp"][a:b]) @ f(o["w_gate"][e]), f"G expert {e}")
+        close(U[a:b], f(o["xp"][a:b]) @ f(o["w_up"][e]), f"U expert {e}")
+        g, u = f(G[a:b]), f(U[a:b])
+        close(H[a:b], g * torch.sigmoid(g) * u, f"H expert {e}")
+        y = f(o["h"][a:b]) @ f(o["w_down"][e])
+        close(Y[a:b], y, f"Y (split tail) expert {e}")
+        close(Yw[a:b], y, f"Y (whole tiles) expert {e}")
+        dh = f(o["dy"][a:b]) @ f(o["w_down"][e]).T
+        gg, uu = f(o["gate"][a:b]), f(o["up"][a:b])
+        sg = torch.sigmoid(gg)
+        close(dG[a:b], dh * uu * sg * (1 + gg * (1 - sg)), f"dG expert {e}")
+        close(dU[a:b], dh * gg * sg, f"dU expert {e}")
+        close(dX[a:b], f(o["dgate"][a:b]) @ f(o["w_gate"][e]).T + f(o["dup"][a:b]) @ f(o["w_up"][e]).T,
+              f"dX expert {e}")
+
+
 WGRAD_CASES = [
     # (counts per expert, D, M): fewer tiles than CUs (most blocks find no tile), and more
     ([5, 0, 300, 64], 256, 256),
