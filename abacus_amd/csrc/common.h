@@ -52,9 +52,14 @@ __device__ inline float hi_bf16(uint32_t w) { return bits_f32(w & 0xffff0000u); 
 // nor before barriers; completion is tracked explicitly with wait_vmcnt<N>().
 // M0 holds the (wave-uniform) LDS destination; lane l's 16 bytes land at
 // M0 + 16 l.
-__device__ inline void dma16(const void* src, char* lds_dst) {
-  const uint32_t lds_addr =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds_dst);
+// dma16_to takes the destination as a wave-uniform LDS byte address, so a
+// caller that converts its LDS base once does the per-DMA address arithmetic
+// in 32-bit scalar registers (a generic pointer costs a 64-bit add and a null
+// check per conversion).
+__device__ inline uint32_t lds_addr32(const void* lds_ptr) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)lds_ptr;
+}
+__device__ inline void dma16_to(const void* src, uint32_t lds_addr) {
   // M0 is reserved by the compiler: save and restore it around the DMA.
   uint32_t saved;
   asm volatile(
@@ -65,6 +70,9 @@ __device__ inline void dma16(const void* src, char* lds_dst) {
       : "=&s"(saved)
       : "v"(src), "s"(lds_addr)
       : "memory");
+}
+__device__ inline void dma16(const void* src, char* lds_dst) {
+  dma16_to(src, __builtin_amdgcn_readfirstlane(lds_addr32(lds_dst)));
 }
 
 // Wait until at most N DMA instructions of this thread are outstanding

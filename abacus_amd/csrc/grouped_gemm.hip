@@ -615,10 +615,10 @@ struct DmaStream {
   // Instruction i of this operand's k-tile at k0.  LDS destinations are
   // wave-uniform: tile + (i * NWAVES + wave) * 1024.
   template <bool MAYBE_RAGGED>
-  __device__ inline void issue_one(int i, char* tile, int wave_u, int k0, int k_lim) const {
+  __device__ inline void issue_one(int i, uint32_t tile, int wave_u, int k0, int k_lim) const {
     const void* src = MC ? (const void*)(base[i] + (int64_t)k0 * ld) : (const void*)(base[i] + k0);
     if (MAYBE_RAGGED && k0 + koff[i] >= k_lim) src = (const void*)g_zero16;
-    dma16(src, tile + (i * NWAVES + wave_u) * 1024);
+    dma16_to(src, tile + (uint32_t)((i * NWAVES + wave_u) * 1024));
   }
 };
 
@@ -943,10 +943,11 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // DMA of k-tile kt: prep(kt) resolves the stage, the k offset and (dual-K)
   // the operand half once; dma(n) sends instruction n of LOADS_PER_TILE (A's
   // first), so the k-loop can place each one between two MFMAs.
-  char* dma_stage = lds;
+  const uint32_t lds32 = lds_addr32(lds);
+  uint32_t dma_stage = lds32;
   int dma_k0 = 0;
   auto prep = [&](int kt) __attribute__((always_inline)) {
-    dma_stage = lds + (kt % ST) * STAGE_BYTES;
+    dma_stage = lds32 + (uint32_t)((kt % ST) * STAGE_BYTES);
     kt += kbase;  // the k-tile within the whole reduction
     const int half = KT::DUAL_K ? (kt >= ktiles_half ? 1 : 0) : 0;
     if (KT::DUAL_K && half != half_set) {  // second half of the concatenated k range
@@ -1355,10 +1356,11 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
   int e = 0, row0 = 0, n0 = 0, k_len = 0, ktiles = 0;
   DmaStream<uint16_t, true, DMA_A> sa;
   DmaStream<uint16_t, true> sb;
-  char* dma_stage = lds;
+  const uint32_t lds32 = lds_addr32(lds);
+  uint32_t dma_stage = lds32;
   int dma_k0 = 0;
   auto prep = [&](int kt) __attribute__((always_inline)) {
-    dma_stage = lds + (kt % STAGES) * STAGE_BYTES;
+    dma_stage = lds32 + (uint32_t)((kt % STAGES) * STAGE_BYTES);
     dma_k0 = kt * BK;
   };
   auto dma = [&](int n) __attribute__((always_inline)) {
