@@ -83,11 +83,11 @@ __device__ inline uint64_t selection_key(float v, int e) {
 }
 
 // ---------------------------------------------------------------------------
-// K1: fused router.  One block = 16 tokens x all experts; the 4 waves split
-// the D reduction (k-blocks interleaved), partials are summed in LDS in a
-// fixed order, the sigmoid and bias are applied per (token, expert), then
-// 16-64 lanes per token run the top-k / renormalise epilogue and bump the
-// block's expert histogram.
+// K1: fused router.  One block = 16 tokens x all experts; the NW waves (4, or
+// 16 for batches of at most kRouterWideT tokens) split the D reduction
+// (k-blocks interleaved), partials are summed in LDS in a fixed order, the
+// sigmoid and bias are applied per (token, expert), then 16 lanes per token
+// run the top-k / renormalise epilogue and bump the block's expert histogram.
 // ---------------------------------------------------------------------------
 // WLDS (bf16, E a multiple of 8): the weight operand comes from w_DE itself.
 // Each wave loads its k-blocks' rows of w_DE (32 x E, zero-padded to EP
@@ -95,8 +95,8 @@ __device__ inline uint64_t selection_key(float v, int e) {
 // (ds_read_b64_tr_b16), so no transposed copy has to be made first; block 0
 // also writes the transposed rows to wt_out, for the backward.  Otherwise the
 // operand is read from wt, the transposed copy.
-template <typename T, int NF, bool WLDS>
-__global__ __launch_bounds__(256) void router_fwd_kernel(
+template <typename T, int NF, bool WLDS, int NW>
+__global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ wt, const T* __restrict__ w_src, T* __restrict__ wt_out,
     const T* __restrict__ bias, int T_, int D, int E, int K,
     float route_scale, T* __restrict__ logits, T* __restrict__ weights, int64_t* __restrict__ indices,
@@ -106,17 +106,18 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   constexpr int EP = NF * 16;
   static_assert(!WLDS || (sizeof(T) == 2 && KB == 32), "the LDS-transposed operand is bf16, 32 k per k-block");
   constexpr int WROW = EP * 2;  // bytes of one staged w row
-  __shared__ float red[4][kRouteTB][EP];
+  constexpr int NTH = NW * 64;
+  __shared__ float red[NW][kRouteTB][EP];
   __shared__ float s_sc[kRouteTB][EP];
   __shared__ float s_sel[kRouteTB][EP];
   __shared__ int s_cnt[EP];
-  __shared__ __align__(16) char s_w[WLDS ? 4 : 1][WLDS ? 32 * WROW : 16];
+  __shared__ __align__(16) char s_w[WLDS ? NW : 1][WLDS ? 32 * WROW : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int t0 = blockIdx.x * kRouteTB;
-  for (int i = tid; i < EP; i += 256) s_cnt[i] = 0;
+  for (int i = tid; i < EP; i += NTH) s_cnt[i] = 0;
 
   f32x4_t acc[NF];
 #pragma unroll
@@ -129,7 +130,8 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   const bool vec_ok = (D % VEC) == 0;  // rows are 16-byte aligned only then
   // U k-blocks per batch, all their loads in flight before their MFMAs: one
   // k-block at a time left the pass waiting out a memory latency per k-block.
-  constexpr int U = NF <= 2 ? 8 : (NF <= 4 ? 4 : (NF <= 8 ? 2 : 1));
+  // (16 waves: at most 4, which at D = 2048 is each wave's whole share)
+  constexpr int U = NF <= 2 && NW <= 4 ? 8 : (NF <= 4 ? 4 : (NF <= 8 ? 2 : 1));
   // WLDS: chunk j of this lane in a k-block = w_DE row c / (EP / 8), 8
   // columns at 8 (c % (EP / 8)), c = lane + 64 j (32 rows x EP / 8 chunks).
   auto load_w = [&](int kbu, Vec16* r) __attribute__((always_inline)) {
@@ -173,15 +175,15 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   };
   int kb0 = wave * KB;
   if (vec_ok) {
-    for (; kb0 + (U - 1) * 4 * KB < D; kb0 += U * 4 * KB) {
+    for (; kb0 + (U - 1) * NW * KB < D; kb0 += U * NW * KB) {
       Vec16 a[U], b[U][NF];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int k = kb0 + u * 4 * KB + kg;
+        const int k = kb0 + u * NW * KB + kg;
         const bool k_ok = k < D;
         a[u] = (row_ok && k_ok) ? ld16(xrow + k) : zero16();
         if constexpr (WLDS) {
-          load_w(kb0 + u * 4 * KB, b[u]);
+          load_w(kb0 + u * NW * KB, b[u]);
         } else {
 #pragma unroll
           for (int f = 0; f < NF; ++f)
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
       for (int u = 0; u < U; ++u) {
         if constexpr (WLDS) {
           Vec16 bf[NF];
-          stage_w(kb0 + u * 4 * KB, b[u], bf);
+          stage_w(kb0 + u * NW * KB, b[u], bf);
 #pragma unroll
           for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a[u], bf[f]);
         } else {
@@ -202,7 +204,7 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
       }
     }
   }
-  for (int kb = kb0; kb < D; kb += 4 * KB) {
+  for (int kb = kb0; kb < D; kb += NW * KB) {
     const int k = kb + kg;
     Vec16 a, b[NF];
     if constexpr (WLDS) {  // vec_ok holds on this path
@@ -239,9 +241,11 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
     for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][f * 16 + (lane & 15)] = acc[f][r];
   __syncthreads();
 
-  for (int i = tid; i < kRouteTB * EP; i += 256) {
+  for (int i = tid; i < kRouteTB * EP; i += NTH) {
     const int tok = i / EP, e = i % EP;
-    const float l = ((red[0][tok][e] + red[1][tok][e]) + red[2][tok][e]) + red[3][tok][e];
+    float l = red[0][tok][e];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) l += red[w][tok][e];
     const int t = t0 + tok;
     if (e < E && t < T_) {
       const float lr = round_to<T>(l);
@@ -253,15 +257,19 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
   }
   __syncthreads();
 
-  // Top-K: L lanes per token (L = 16, 32 or 64 as EP allows; 64 / L tokens
-  // per wave at once), lane j of a token holding experts j, j + L, ... as
-  // selection keys.  Each of the K rounds takes the maximum key over the
-  // token's lanes and retires that expert.
-  constexpr int L = EP >= 64 ? 64 : (EP <= 16 ? 16 : (EP <= 32 ? 32 : 64));
+  // Top-K: L lanes per token, lane j of a token holding experts j, j + L, ...
+  // as selection keys.  Each of the K rounds takes the maximum key over the
+  // token's lanes (a local maximum, then log2(L) butterfly steps) and retires
+  // that expert.  The rounds are a chain of dependent lane shuffles, so up to
+  // 64 experts a token gets 16 lanes (4 tokens per wave at once, a block's 16
+  // tokens in one pass; with 64 lanes, 6 steps and a token per pass, this
+  // epilogue took most of the kernel's ~28 us at small batches); beyond 64
+  // experts, 64 lanes keep the keys per lane (and registers) few.
+  constexpr int L = EP <= 64 ? 16 : 64;
   constexpr int TPW = 64 / L;                  // tokens per wave pass
   constexpr int CPL = EP <= L ? 1 : EP / L;    // experts per lane
   const int sub = lane / L, ln = lane % L;
-  for (int tok0 = wave * TPW; tok0 < kRouteTB; tok0 += 4 * TPW) {
+  for (int tok0 = wave * TPW; tok0 < kRouteTB; tok0 += NW * TPW) {
     const int tok = tok0 + sub;
     const int t = t0 + tok;
     const bool valid = t < T_;
@@ -307,7 +315,7 @@ __global__ __launch_bounds__(256) void router_fwd_kernel(
     }
   }
   __syncthreads();
-  for (int e = tid; e < E; e += 256) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+  for (int e = tid; e < E; e += NTH) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
 }
 
 // ---------------------------------------------------------------------------
@@ -624,44 +632,69 @@ __device__ __attribute__((always_inline)) inline void for_each_sorted_slot(int t
 // Row vectors per lane whose loads of one slot are in flight together in the
 // wave-per-token gather kernels.
 constexpr int kGatherBatch = 4;
+// Batches of at most this many tokens combine in column chunks (a wave per
+// token and 64-vector chunk, every slot's loads in flight at once).
+constexpr int64_t kCombineSmallT = 1024;
+// Batches of at most this many tokens run the router with 16 waves per block.
+constexpr int64_t kRouterWideT = 1024;
 
 // ---------------------------------------------------------------------------
 // K6: combine.  out[t] = sum_k round(y[pos(t,k)] * w(t,k)), experts ascending,
 // fp32 accumulation, one rounding (the stack().sum(0) of moe.py:85).
 // Gather-reduce per token: no atomics, deterministic.
 // ---------------------------------------------------------------------------
-template <typename T, int KB>
+template <typename T, int KB, bool SMALL>
 __global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ y, const T* __restrict__ weights,
                                                           const int32_t* __restrict__ idx,
                                                           const int32_t* __restrict__ pos, int T_, int D, int K,
                                                           T* __restrict__ out) {
-  // one token per wave: no barrier between the slot reads and the row reads,
-  // and kGatherBatch row vectors of a slot in flight per lane
+  // one token per wave: no barrier between the slot reads and the row reads.
+  // Large batches: kGatherBatch row vectors of a slot in flight per lane, the
+  // slots one after another.  SMALL (few tokens, K <= 8): blockIdx.y picks
+  // 64-vector column chunks of the token, so more waves share the rows, and
+  // a lane's vectors of every slot are in flight at once (one memory latency
+  // per chunk instead of one per slot).  Same sums in the same order.
   constexpr int VEC = VecTraits<T>::kN;
-  constexpr int U = kGatherBatch;
+  constexpr int U = SMALL ? 1 : kGatherBatch;
+  static_assert(!SMALL || KB <= 8, "all slots in registers");
   const int lane = threadIdx.x & 63;
   const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (t >= T_) return;
   auto coef = [&](int64_t i) { return to_f32<T>(weights[i]); };
   const int nvec = D / VEC;
-  for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
+  for (int c0 = (int)blockIdx.y * 64 * U; c0 < nvec; c0 += (int)gridDim.y * 64 * U) {
     float acc[U][VEC];
 #pragma unroll
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int i = 0; i < VEC; ++i) acc[u][i] = 0.f;
-    for_each_sorted_slot<KB>(t, K, idx, pos, coef, [&](int pk, int, float wk) __attribute__((always_inline)) {
-      Vec16 v[U];
+    if constexpr (SMALL) {
+      int e[KB], p[KB];
+      float w[KB];
+      token_slots_by_expert<KB>(t, K, idx, pos, coef, e, p, w);
+      const int c = c0 + lane;
+      Vec16 v[KB];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int c = c0 + u * 64 + lane;
-        v[u] = c < nvec ? ld16(y + (int64_t)pk * D + c * VEC) : zero16();
-      }
+      for (int k = 0; k < KB; ++k) v[k] = k < K && c < nvec ? ld16(y + (int64_t)p[k] * D + c * VEC) : zero16();
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int k = 0; k < KB; ++k)
+        if (k < K)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) acc[u][i] += round_to<T>(VecTraits<T>::get(v[u], i) * wk);
-    });
+          for (int i = 0; i < VEC; ++i) acc[0][i] += round_to<T>(VecTraits<T>::get(v[k], i) * w[k]);
+    } else {
+      for_each_sorted_slot<KB>(t, K, idx, pos, coef, [&](int pk, int, float wk) __attribute__((always_inline)) {
+        Vec16 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = c0 + u * 64 + lane;
+          v[u] = c < nvec ? ld16(y + (int64_t)pk * D + c * VEC) : zero16();
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) acc[u][i] += round_to<T>(VecTraits<T>::get(v[u], i) * wk);
+      });
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = c0 + u * 64 + lane;
@@ -1422,23 +1455,34 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   }
   if (nb == 0) return 0;
   if (wlds) {
-#define ROUTER_LAUNCH_W(NF)                                                                                           \
-  hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true>), dim3(nb), dim3(256), 0, s, (const uint16_t*)x_TD,      \
-                     (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws, (const uint16_t*)bias_E,      \
-                     (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE, (uint16_t*)weights_TK,        \
-                     indices_TK, idx_TK, score_TK, hist)
-    switch (EP / 16) {
-      case 1: ROUTER_LAUNCH_W(1); break;
-      case 2: ROUTER_LAUNCH_W(2); break;
-      case 3: ROUTER_LAUNCH_W(3); break;
-      default: ROUTER_LAUNCH_W(4); break;
+#define ROUTER_LAUNCH_W(NF, NW)                                                                                      \
+  hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true, NW>), dim3(nb), dim3(NW * 64), 0, s,                      \
+                     (const uint16_t*)x_TD, (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws,        \
+                     (const uint16_t*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE,      \
+                     (uint16_t*)weights_TK, indices_TK, idx_TK, score_TK, hist)
+    // small batches: 16 waves per block split D four times finer, so each
+    // wave's loads are one batch in flight instead of a chain of batches
+    if (T <= kRouterWideT) {
+      switch (EP / 16) {
+        case 1: ROUTER_LAUNCH_W(1, 16); break;
+        case 2: ROUTER_LAUNCH_W(2, 16); break;
+        case 3: ROUTER_LAUNCH_W(3, 16); break;
+        default: ROUTER_LAUNCH_W(4, 16); break;
+      }
+    } else {
+      switch (EP / 16) {
+        case 1: ROUTER_LAUNCH_W(1, 4); break;
+        case 2: ROUTER_LAUNCH_W(2, 4); break;
+        case 3: ROUTER_LAUNCH_W(3, 4); break;
+        default: ROUTER_LAUNCH_W(4, 4); break;
+      }
     }
 #undef ROUTER_LAUNCH_W
     ABACUS_CHECK_LAUNCH("router_fwd");
     return 0;
   }
 #define ROUTER_LAUNCH(TT, NF)                                                                                      \
-  hipLaunchKernelGGL((router_fwd_kernel<TT, NF, false>), dim3(nb), dim3(256), 0, s, (const TT*)x_TD,              \
+  hipLaunchKernelGGL((router_fwd_kernel<TT, NF, false, 4>), dim3(nb), dim3(256), 0, s, (const TT*)x_TD,           \
                      (const TT*)wt_ws, (const TT*)nullptr, (TT*)nullptr, (const TT*)bias_E, (int)T, (int)D, (int)E, \
                      (int)K, route_scale, (TT*)logits_TE, (TT*)weights_TK, indices_TK, idx_TK, score_TK, hist)
 #define ROUTER_DISPATCH_NF(TT)          \
@@ -1546,14 +1590,24 @@ int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32
   hipStream_t s = (hipStream_t)stream;
   ABACUS_CHECK_ARG(T <= (int64_t)INT_MAX - 3, "too many tokens (%lld)", (long long)T);
   const unsigned grid = (unsigned)((T + 3) / 4);  // a token per wave
+  // small batches (fewer tokens than 4 per CU): a block per 64-vector column
+  // chunk as well
+  const int64_t nvec = D / vec_elems(dtype);
+  const bool small = T <= kCombineSmallT && K <= 8;
+  const dim3 g(grid, small ? (unsigned)((nvec + 63) / 64) : 1u);
   with_slot_bound(K, [&](auto kb) {
     constexpr int KB = decltype(kb)::value;
-    if (dtype == kBF16)
-      hipLaunchKernelGGL((combine_fwd_kernel<uint16_t, KB>), dim3(grid), dim3(256), 0, s, (const uint16_t*)y_RD,
-                         (const uint16_t*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (uint16_t*)out_TD);
-    else
-      hipLaunchKernelGGL((combine_fwd_kernel<float, KB>), dim3(grid), dim3(256), 0, s, (const float*)y_RD,
-                         (const float*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (float*)out_TD);
+    auto launch = [&](auto sm) {
+      constexpr bool SMALL = decltype(sm)::value && KB <= 8;
+      if (dtype == kBF16)
+        hipLaunchKernelGGL((combine_fwd_kernel<uint16_t, KB, SMALL>), g, dim3(256), 0, s, (const uint16_t*)y_RD,
+                           (const uint16_t*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (uint16_t*)out_TD);
+      else
+        hipLaunchKernelGGL((combine_fwd_kernel<float, KB, SMALL>), g, dim3(256), 0, s, (const float*)y_RD,
+                           (const float*)weights_TK, idx_TK, pos_TK, (int)T, (int)D, (int)K, (float*)out_TD);
+    };
+    if (small) launch(std::true_type());
+    else launch(std::false_type());
   });
   ABACUS_CHECK_LAUNCH("combine_fwd");
   return 0;
