@@ -516,27 +516,38 @@ constexpr int DMA_PER_OPERAND = TILE_CHUNKS / NT;   // 16-byte chunks per thread
 constexpr int LOADS_PER_TILE = 2 * DMA_PER_OPERAND; // DMA instructions per thread per k-tile
 
 // Row-grouped kinds cut each expert's rows into BM-row tiles; a remainder of
-// at most THIN rows goes to a thin tile of THIN rows (same 256 columns, same
-// MFMAs and k order, so the same results) instead of a mostly empty full one.
-// Thin tiles run a 3-stage ring (3 x 48 KB): with few rows per expert they
-// mostly stream weights, and a third stage doubles the DMA a CU keeps in
-// flight (gate/up forward at 6 rows per expert 205 -> 184 us; Mixtral's
-// remainder tiles 1889 -> 1847 us).  Full tiles keep 2 stages (2 x 64 KB).
+// at most THIN rows goes to a thin tile of THIN rows (same MFMAs and k order,
+// so the same results) instead of a mostly empty full one.  bf16 thin tiles
+// keep 256 columns and a 3-stage ring of 48 KB stages: with few rows per
+// expert they mostly stream weights, and a third stage doubles the DMA a CU
+// keeps in flight (gate/up forward at 6 rows per expert 205 -> 184 us;
+// Mixtral's remainder tiles 1889 -> 1847 us); 128-column thin tiles measured
+// slower there (more, shorter weight-row segments per tile: T = 512 gate/up
+// 177 -> 190 us).  fp32 thin tiles have 128 columns and 4 stages of 32 KB (the
+// fp32 gate/up data gradient 3885 -> 3566 us at the mid-size layer).  Full
+// tiles keep 2 stages (2 x 64 KB).
 constexpr int THIN = 128;
-constexpr int THIN_STAGES = 3;
-template <int BMT>
+template <typename T> constexpr int kThinN = sizeof(T) == 4 ? 128 : 256;
+template <typename T> constexpr int kThinStages = sizeof(T) == 4 ? 4 : 3;
+template <int BMT, typename T = uint16_t>
 struct Geo {
   static_assert(BMT == BM || BMT == THIN, "full or thin tiles");
   static constexpr int WTM = BMT / WAVES_M, FM = WTM / 32;
+  static constexpr int BN = BMT == BM ? pipe::BN : kThinN<T>;  // tile columns
+  static constexpr int WTN = BN / WAVES_N, FN = WTN / 32;
+  static constexpr int LDC = BN + 8;                           // epilogue C tile row stride (bf16)
   static constexpr int A_BYTES = BMT * BK * 2;                 // A operand tile
-  static constexpr int STAGE = A_BYTES + TILE_BYTES;           // A + B
-  static constexpr int ST = BMT == BM ? STAGES : THIN_STAGES;  // ring depth
-  static constexpr int DMA_A = A_BYTES / 16 / NT, DMA_B = DMA_PER_OPERAND;
+  static constexpr int B_BYTES = BN * BK * 2;                  // B operand tile
+  static constexpr int STAGE = A_BYTES + B_BYTES;              // A + B
+  static constexpr int ST = BMT == BM ? STAGES : kThinStages<T>;  // ring depth
+  static constexpr int DMA_A = A_BYTES / 16 / NT, DMA_B = B_BYTES / 16 / NT;
   static constexpr int LOADS = DMA_A + DMA_B;                  // DMA instructions per thread per k-tile
   static constexpr int LDS = ST * STAGE > BMT * LDC * 2 ? ST * STAGE : BMT * LDC * 2;
 };
 static_assert(Geo<BM>::LDS == LDS_BYTES, "full tiles");
-constexpr int LDS_ALLOC = Geo<THIN>::LDS > LDS_BYTES ? Geo<THIN>::LDS : LDS_BYTES;
+constexpr int kThinLds = Geo<THIN, uint16_t>::LDS > Geo<THIN, float>::LDS ? Geo<THIN, uint16_t>::LDS
+                                                                          : Geo<THIN, float>::LDS;
+constexpr int LDS_ALLOC = kThinLds > LDS_BYTES ? kThinLds : LDS_BYTES;
 static_assert(LDS_ALLOC <= 160 * 1024, "LDS is 160 KB per work-group");
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
@@ -548,14 +559,17 @@ __device__ __attribute__((aligned(16))) uint32_t g_zero16[4];
 // kc rows are CPR chunks; 256 bytes of LDS banks hold 16 / CPR rows, so rows
 // of one bank period get distinct chunk permutations.
 __device__ inline int kc_off(int row, int chunk) { return (row * CPR + (chunk ^ ((row / (16 / CPR)) % CPR))) * 16; }
-__device__ inline int mc_off(int k, int chunk) { return (k * 32 + (chunk ^ ((k & 3) << 2))) * 16; }
-// The mn-contiguous tile of fp32 operands: [32 k][64 chunks] (the same 32 KB),
-// chunks XOR-swizzled by groups of 8 per 4 k rows so that the two half-waves
-// of a fragment read (rows k and k + 4) hit different banks.
-__device__ inline int mc_off32(int k, int chunk) { return (k * 64 + (chunk ^ (((k >> 2) & 7) << 3))) * 16; }
-template <typename T> __device__ inline int mc_swz(int k);
-template <> __device__ inline int mc_swz<uint16_t>(int k) { return (k & 3) << 2; }
-template <> __device__ inline int mc_swz<float>(int k) { return ((k >> 2) & 7) << 3; }
+// The mn-contiguous tile: [k][MCC chunks] (MCC = 16-byte chunks per k row,
+// 32 for a 256-wide bf16 tile), chunks XOR-swizzled per k row.  bf16: by
+// (k % 4) * 4.  fp32: by groups of 8 chunks per 4 k rows, so that the two
+// half-waves of a fragment read (rows k and k + 4) hit different banks.
+template <typename T, int MCC> __device__ inline int mc_swz(int k);
+template <> __device__ inline int mc_swz<uint16_t, 16>(int k) { return (k & 3) << 2; }
+template <> __device__ inline int mc_swz<uint16_t, 32>(int k) { return (k & 3) << 2; }
+template <> __device__ inline int mc_swz<float, 32>(int k) { return ((k >> 2) & 3) << 3; }
+template <> __device__ inline int mc_swz<float, 64>(int k) { return ((k >> 2) & 7) << 3; }
+template <typename T, int MCC>
+__device__ inline int mc_off(int k, int chunk) { return (k * MCC + (chunk ^ mc_swz<T, MCC>(k))) * 16; }
 // k-tile depth in elements: 128 bytes of k per row for either dtype
 template <typename T> constexpr int kBKT = 128 / (int)sizeof(T);
 static_assert(kBKT<uint16_t> == BK, "the bf16 k-tile");
@@ -575,10 +589,10 @@ __device__ inline float sigmoid_hw(float x) { return __builtin_amdgcn_rcpf(1.0f 
 // source pointers once and issue() adds the k0 step (kc: k0 elements, mc:
 // k0 rows) -- one 64-bit add per DMA.  Chunks whose k lies beyond k_lim
 // (a ragged segment's tail) read the zero page instead.
-template <typename T, bool MC, int N = DMA_PER_OPERAND>
+template <typename T, bool MC, int N = DMA_PER_OPERAND, int BNT = BN>
 struct DmaStream {
-  static constexpr int EPC = 16 / (int)sizeof(T);       // elements per 16-byte chunk
-  static constexpr int MCC = BN * (int)sizeof(T) / 16;  // chunks per mn-contiguous k row
+  static constexpr int EPC = 16 / (int)sizeof(T);        // elements per 16-byte chunk
+  static constexpr int MCC = BNT * (int)sizeof(T) / 16;  // chunks per mn-contiguous k row
   const T* base[N];
   int koff[N];   // k of the chunk relative to k0
   int64_t ld;
@@ -597,12 +611,12 @@ struct DmaStream {
         koff[i] = c * EPC;
       } else {
         const int k = p / MCC;
-        const int c = (p % MCC) ^ mc_swz<T>(k);
+        const int c = (p % MCC) ^ mc_swz<T, MCC>(k);
         int mn = c * EPC;
         const T* b = b0;
-        if (b1 != nullptr && mn >= BN / 2) {
+        if (b1 != nullptr && mn >= BNT / 2) {
           b = b1;
-          mn -= BN / 2;
+          mn -= BNT / 2;
         }
         int gm = r0 + mn;
         gm = gm < r_lim ? gm : r_lim - EPC;
@@ -627,28 +641,32 @@ __device__ inline Vec16 frag_kc(const char* tile, int f0, int t, int lane) {
   const int r = f0 + (lane & 31);
   return *reinterpret_cast<const Vec16*>(tile + kc_off(r, 2 * t + (lane >> 5)));
 }
-template <typename T> __device__ inline Vec16 frag_mc(const char* tile, int f0, int t, int lane);
-// fp32: lane l gets the 4 k at 8 t + 4 (l / 32) of column f0 + l % 32 (one
-// 32-bit read each; the MFMA's k order, as frag_kc's 16-byte chunk)
-template <> __device__ inline Vec16 frag_mc<float>(const char* tile, int f0, int t, int lane) {
-  const int cc = f0 + (lane & 31), k0 = 8 * t + 4 * (lane >> 5);
+// 32 x 16 MFMA operand fragment of an mn-contiguous tile (MCC chunks per k
+// row).  fp32: lane l gets the 4 k at 8 t + 4 (l / 32) of column f0 + l % 32
+// (one 32-bit read each; the MFMA's k order, as frag_kc's 16-byte chunk).
+// bf16: two transposed reads (ds_read_b64_tr_b16) of 4 k each.
+template <typename T, int MCC>
+__device__ inline Vec16 frag_mc(const char* tile, int f0, int t, int lane) {
   Vec16 v;
+  if constexpr (sizeof(T) == 4) {
+    const int cc = f0 + (lane & 31), k0 = 8 * t + 4 * (lane >> 5);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v.w[j] = *reinterpret_cast<const uint32_t*>(tile + mc_off32(k0 + j, cc >> 2) + (cc & 3) * 4);
-  return v;
-}
-template <> __device__ inline Vec16 frag_mc<uint16_t>(const char* tile, int f0, int t, int lane) {
-  const int grp = lane >> 4, s = lane & 15;
-  const int mn = f0 + 16 * (grp & 1) + 4 * (s & 3);
-  const int k = 16 * t + 8 * (grp >> 1) + (s >> 2);
-  const int b = (mn & 7) * 2;
-  const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(tile + mc_off(k, mn >> 3) + b));
-  const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(tile + mc_off(k + 4, mn >> 3) + b));
-  Vec16 v;
-  v.w[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
-  v.w[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
-  v.w[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
-  v.w[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+    for (int j = 0; j < 4; ++j)
+      v.w[j] = *reinterpret_cast<const uint32_t*>(tile + mc_off<T, MCC>(k0 + j, cc >> 2) + (cc & 3) * 4);
+  } else {
+    const int grp = lane >> 4, s = lane & 15;
+    const int mn = f0 + 16 * (grp & 1) + 4 * (s & 3);
+    const int k = 16 * t + 8 * (grp >> 1) + (s >> 2);
+    const int b = (mn & 7) * 2;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(tile + mc_off<T, MCC>(k, mn >> 3) + b));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16*)(tile + mc_off<T, MCC>(k + 4, mn >> 3) + b));
+    v.w[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+    v.w[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+    v.w[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+    v.w[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+  }
   return v;
 }
 
@@ -871,10 +889,13 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   using KT = KindTraits<KIND>;
   using Op = MfmaOp<T, 32>;
   constexpr int BKT = kBKT<T>;  // k-tile depth in elements
-  using GE = Geo<BMT>;
+  using GE = Geo<BMT, T>;
   static_assert(!KT::WGRAD || BMT == BM, "weight gradients have full tiles only");
   constexpr int FM = GE::FM, WTM = GE::WTM, STAGE_BYTES = GE::STAGE, A_BYTES = GE::A_BYTES;
-  constexpr int LOADS_PER_TILE = GE::LOADS, DMA_A = GE::DMA_A, ST = GE::ST;
+  constexpr int LOADS_PER_TILE = GE::LOADS, DMA_A = GE::DMA_A, DMA_B = GE::DMA_B, ST = GE::ST;
+  // this tile geometry's columns (they hide the full tiles' namespace values)
+  constexpr int BN = GE::BN, WTN = GE::WTN, FN = GE::FN, LDC = GE::LDC;
+  constexpr int MCC_A = BMT * (int)sizeof(T) / 16, MCC_B = BN * (int)sizeof(T) / 16;  // mn-contiguous rows
   static_assert(!KindTraits<KIND>::DUAL_B || FN % 2 == 0, "dual-B pairs gate/up fragments");
   constexpr int BNH = KT::DUAL_B ? BN / 2 : BN;   // output columns per tile (per half)
 
@@ -935,8 +956,8 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
 
   // wave index as a scalar so the DMA destinations are computed in SGPRs
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  DmaStream<T, KT::A_MC, DMA_A> sa;
-  DmaStream<T, KT::B_NC> sb;
+  DmaStream<T, KT::A_MC, DMA_A, BMT> sa;
+  DmaStream<T, KT::B_NC, DMA_B, BN> sb;
   int half_set = 0;
   sa.setup(A0, nullptr, g.lda, row0, a_lim, wave, lane);
   sb.setup(B0, KT::DUAL_B ? B1 : nullptr, g.ldb, n0, g.Ndim, wave, lane);
@@ -990,10 +1011,10 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     const char* Bt = st + A_BYTES;
     if (f == 0 || f > FN) {
       const int i = f == 0 ? 0 : f - FN;
-      af[slot][i] = KT::A_MC ? frag_mc<T>(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
+      af[slot][i] = KT::A_MC ? frag_mc<T, MCC_A>(At, wm * WTM + i * 32, t, lane) : frag_kc(At, wm * WTM + i * 32, t, lane);
     } else {
       const int j = f - 1;
-      bfr[slot][j] = KT::B_NC ? frag_mc<T>(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
+      bfr[slot][j] = KT::B_NC ? frag_mc<T, MCC_B>(Bt, b_col(j), t, lane) : frag_kc(Bt, b_col(j), t, lane);
     }
   };
 
@@ -1156,7 +1177,7 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   constexpr int VEC = 8;
   constexpr int CV = BNH / VEC;
   constexpr int NV = BMT * CV / NT;  // vectors per thread
-  constexpr int BATCH = 8;
+  constexpr int BATCH = NV < 8 ? NV : 8;
   constexpr int NBATCH = NV / BATCH;
   static_assert(NV % BATCH == 0, "whole batches");
   const int rlim = KT::WGRAD ? g.Mdim : row_end;
@@ -1401,10 +1422,10 @@ __device__ __attribute__((always_inline)) inline void gemm_wgrad_tiles(const Gem
   auto read_frag = [&](const char* st, int t, int slot, int f) __attribute__((always_inline)) {
     if (f == 0 || f > FN) {
       const int i = f == 0 ? 0 : f - FN;
-      af[slot][i] = frag_mc<uint16_t>(st, wm * WTM + i * 32, t, lane);
+      af[slot][i] = frag_mc<uint16_t, 32>(st, wm * WTM + i * 32, t, lane);
     } else {
       const int j = f - 1;
-      bfr[slot][j] = frag_mc<uint16_t>(st + A_BYTES, b_col(j), t, lane);
+      bfr[slot][j] = frag_mc<uint16_t, 32>(st + A_BYTES, b_col(j), t, lane);
     }
   };
   // The k-step and k-tile schedule of gemm_tile, repeated: sharing one helper
@@ -1678,10 +1699,11 @@ int64_t wgrad_blocks(GemmArgs& g, int R) {
 
 // The thin row tiles of a row-grouped kind: at most one per expert, in the
 // same column tiles.  Returns the number of blocks, a multiple of 8.
-template <int KIND>
+template <typename T, int KIND>
 int64_t pipe_grid_thin(GemmArgs& g, int R) {
   static_assert(!KindTraits<KIND>::WGRAD, "row-grouped kinds");
-  pipe_grid<KIND>(g, R);  // sizes tiles_n
+  constexpr int BNH = KindTraits<KIND>::DUAL_B ? pipe::kThinN<T> / 2 : pipe::kThinN<T>;
+  g.tiles_n = pipe::round_up((g.Ndim + BNH - 1) / BNH, pipe::GN);
   const int mt = std::min(g.E, R);  // at most one thin tile per expert with rows
   if (mt == 0 || g.tiles_n == 0) return 0;
   g.tiles_m = pipe::round_up(mt, pipe::GM);
@@ -1699,7 +1721,7 @@ int launch_rows(const GemmArgs& g1, int R, const GemmArgs* gw, int64_t n1, bool 
   ga.thin = gt.thin = thin ? 1 : 0;
   const int64_t full = pipe_grid<KR>(ga, R);
   if (n1 < 0) n1 = full;  // no split: one block per full tile of the upper bound
-  const int64_t n2 = thin ? pipe_grid_thin<KR>(gt, R) : 0;
+  const int64_t n2 = thin ? pipe_grid_thin<T, KR>(gt, R) : 0;
   int64_t n3 = 0;
   if constexpr (KW >= 0) {
     n3 = wgrad_blocks<KW>(gc, R);
