@@ -1159,8 +1159,15 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
             }
             *reinterpret_cast<float4*>((float*)g.c0 + o) = make_float4(dg[0], dg[1], dg[2], dg[3]);
             *reinterpret_cast<float4*>((float*)g.c1 + o) = make_float4(du[0], du[1], du[2], du[3]);
+          } else if constexpr (KT::WGRAD) {
+            // expert e's weight gradient; dual-B: fragment j + JN is the up half
+            const int64_t oe = (int64_t)e * g.c_estride + o;
+            *reinterpret_cast<float4*>((float*)g.c0 + oe) = c0;
+            if constexpr (KT::DUAL_B)
+              *reinterpret_cast<float4*>((float*)g.c1 + oe) =
+                  make_float4(acc[i][j + JN][4 * gq], acc[i][j + JN][4 * gq + 1], acc[i][j + JN][4 * gq + 2],
+                              acc[i][j + JN][4 * gq + 3]);
           } else {
-            static_assert(!KT::WGRAD, "fp32 weight gradients run on the generic kernel");
             *reinterpret_cast<float4*>((float*)g.c0 + o) = c0;
           }
         }
@@ -1549,6 +1556,17 @@ __global__ __launch_bounds__(NT, 1) void gemm_bf16_wgrad_kernel(GemmArgs g) {
   gemm_wgrad_tiles<KIND>(g, lds, &next_s, offs_s);
 }
 
+// fp32 weight gradients: one block per tile of the (expert, row tile, column
+// tile) space.  An fp32 tile's reduction over ~1000 rows is 32 k-tiles of
+// 32, ~30x a tile's prologue and epilogue, so the persistent loop of the bf16
+// weight gradients would gain little here.
+template <typename T, int KIND>
+__global__ __launch_bounds__(NT, 1) void gemm_tiles_kernel(GemmArgs g) {
+  static_assert(KindTraits<KIND>::WGRAD && sizeof(T) == 4, "fp32 weight gradients");
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_ALLOC];
+  gemm_tile<T, KIND, BM>(g, (int)blockIdx.x, (int)gridDim.x, lds, nullptr);
+}
+
 // A row-grouped kind's full tiles, then its thin tiles, then (KW >= 0) a
 // weight gradient's tiles, in one launch: blocks [0, n1), [n1, n1 + n2), and
 // the rest (n1 and n2 multiples of 8), the last as a persistent loop
@@ -1746,8 +1764,15 @@ int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
     // (the down projection's forward reduces over M: its tiles are long, and
     // thin ones would end the launch on a partial round of them)
     return launch_rows<T, KIND, -1>(g, R, nullptr, -1, KIND != kDownFwd, s, name);
+  } else if constexpr (sizeof(T) == 4) {
+    GemmArgs ga = g;
+    const int64_t blocks = pipe_grid<KIND>(ga, R);
+    if (blocks == 0) return 0;
+    ABACUS_CHECK_ARG(blocks < (1ll << 31), "%s: tile grid too large", name);
+    hipLaunchKernelGGL((pipe::gemm_tiles_kernel<float, KIND>), dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
+    ABACUS_CHECK_LAUNCH(name);
+    return 0;
   } else {
-    static_assert(sizeof(T) == 2, "pipelined weight gradients: bf16");
     GemmArgs ga = g;
     const int64_t blocks = wgrad_blocks<KIND>(ga, R);
     if (blocks == 0) return 0;
@@ -1831,23 +1856,28 @@ int launch_pipe_pair(const GemmArgs& a, int Ra, const GemmArgs& b, int Rb, hipSt
 // of k-tiles (always true for the workloads; the generic kernel covers the
 // rest).  The routed-row count of a row-grouped kind is free: its tiles clamp
 // their row addresses to the expert's last row.  bf16: every kind.  fp32:
-// the gate/up forward and data gradient and the down projection's forward,
-// once the rows fill at least one round of 256 x 256 tiles over the CUs
-// (below that the generic kernel's 128 x 128 tiles reach more CUs); the fp32
-// down-projection data gradient, whose epilogue also reads G and U, and the
-// fp32 weight gradients measured faster on the generic kernel.
+// the gate/up forward and data gradient, the down projection's forward and
+// the weight gradients (one block per tile), once there is at least one
+// round of 256 x 256 tiles over the CUs (below that the generic kernel's
+// 128 x 128 tiles reach more CUs); the fp32 down-projection data gradient,
+// whose epilogue also reads G and U, measured faster on the generic kernel.
 template <int KIND>
 bool pipe_ok(int dtype, const GemmArgs& g, int R) {
   using KT = KindTraits<KIND>;
   if (g.Ndim % 8 != 0 || (KT::WGRAD && g.Mdim % 8 != 0)) return false;
   if (dtype == kBF16) return KT::WGRAD || g.Kdim % pipe::BK == 0;
-  if (dtype != kF32 || KT::WGRAD || KIND == kDownDgrad || g.Kdim % pipe::kBKT<float> != 0) return false;
   constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
+  if (dtype == kF32 && KT::WGRAD)  // one round of per-expert tiles
+    return (int64_t)g.E * ((g.Mdim + pipe::BM - 1) / pipe::BM) * ((g.Ndim + BNH - 1) / BNH) >= cu_count();
+  if (dtype != kF32 || KIND == kDownDgrad || g.Kdim % pipe::kBKT<float> != 0) return false;
   return (int64_t)((R + pipe::BM - 1) / pipe::BM) * ((g.Ndim + BNH - 1) / BNH) >= cu_count();
 }
 
 template <int KIND>
 int dispatch_gemm(int dtype, const GemmArgs& g, int R, hipStream_t s, const char* name) {
+  if constexpr (KindTraits<KIND>::WGRAD) {
+    if (dtype == kF32 && pipe_ok<KIND>(dtype, g, R)) return launch_pipe<float, KIND>(g, R, s, name);
+  }
   if constexpr (KIND == kGateUpWgrad) {
     // fp32 on the generic kernel: dW_gate and dW_up as two single weight
     // gradients (x^T dG, x^T dU: the down projection's kind with other
