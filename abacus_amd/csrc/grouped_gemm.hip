@@ -1114,40 +1114,70 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     return;
   }
   if constexpr (sizeof(T) == 4) {
-    // fp32: straight from the accumulators (a 256 x 256 fp32 C tile does not
-    // fit in LDS, and the main loop is long enough that the scattered 16-byte
-    // stores cost little).  Fragment (i, j) holds C^T: lane l has row l % 32
-    // and, for gq = 0..3, columns 8 gq + 4 (l / 32) .. +3.  Same elementwise
-    // epilogues as the generic kernel's fp32 path.
+    // fp32: the C tile (256 KB for 256 x 256) does not fit in LDS, so it goes
+    // out in bands of RB rows: the waves holding a band's rows write their
+    // fragments to LDS, then every thread takes row-major 16-byte vectors of
+    // the band, so the stores (and the down projection's G and U loads) are
+    // whole rows rather than 32-byte pieces.  Fragment (i, j) holds C^T: lane
+    // l has row l % 32 and, for gq = 0..3, columns 8 gq + 4 (l / 32) .. +3.
+    // Same elementwise epilogues as the generic kernel's fp32 path.
+    constexpr int RB = 128;                  // band rows (a wave row of full tiles, a whole thin tile)
+    static_assert(BMT % RB == 0 && (WTM % RB == 0 || RB % WTM == 0), "bands of whole wave rows");
+    constexpr int LDB = BN + 4;              // band row stride in floats
+    static_assert(RB * LDB * 4 <= LDS_ALLOC, "an fp32 band fits in LDS");
+    constexpr int CV4 = BNH / 4;             // float4 vectors per band row (per half)
+    constexpr int NV4 = RB * CV4 / NT;       // per thread
+    constexpr int BAT = NV4 < 8 ? NV4 : 8;   // global loads in flight per thread (down backward)
+    static_assert(NV4 % BAT == 0 && NT % CV4 == 0, "whole batches; a thread keeps one band column");
+    float* band = reinterpret_cast<float*>(lds);
     const int rl = lane & 31, ch = 4 * (lane >> 5);
     const int rlim = KT::WGRAD ? g.Mdim : row_end;
-    constexpr int JN = KT::DUAL_B ? FN / 2 : FN;
+    __syncthreads();  // every fragment read done: the bands overwrite the stages
 #pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int row = row0 + wm * WTM + i * 32 + rl;
-      if (row >= rlim) continue;
+    for (int pb = 0; pb < BMT / RB; ++pb) {
+      if (wm * WTM / RB == pb) {
 #pragma unroll
-      for (int j = 0; j < JN; ++j)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const int col = n0 + b_col(j) + 8 * gq + ch;  // dual-B: the gate half; fragment j + JN is up
-          if (col >= g.Ndim) continue;
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+              *reinterpret_cast<float4*>(band + (wm * WTM - pb * RB + i * 32 + rl) * LDB + b_col(j) + 8 * gq + ch) =
+                  make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2], acc[i][j][4 * gq + 3]);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int b0 = 0; b0 < NV4; b0 += BAT) {
+        float4 gi[BAT], ui[BAT];
+        if constexpr (KIND == kDownDgrad) {
+#pragma unroll
+          for (int u = 0; u < BAT; ++u) {
+            const int v = tid + (b0 + u) * NT, r = v / CV4, c = (v % CV4) * 4;
+            const int row = row0 + pb * RB + r, col = n0 + c;
+            if (row < rlim && col < g.Ndim) {
+              const int64_t o = (int64_t)row * g.ldc + col;
+              gi[u] = *reinterpret_cast<const float4*>((const float*)g.x0 + o);
+              ui[u] = *reinterpret_cast<const float4*>((const float*)g.x1 + o);
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < BAT; ++u) {
+          const int v = tid + (b0 + u) * NT, r = v / CV4, c = (v % CV4) * 4;
+          const int row = row0 + pb * RB + r, col = n0 + c;
+          if (row >= rlim || col >= g.Ndim) continue;
           const int64_t o = (int64_t)row * g.ldc + col;
-          const float4 c0 = make_float4(acc[i][j][4 * gq], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
-                                        acc[i][j][4 * gq + 3]);
+          const float4 c0 = *reinterpret_cast<const float4*>(band + r * LDB + c);
           if constexpr (KIND == kGateUpFwd) {
-            const float4 c1 = make_float4(acc[i][j + JN][4 * gq], acc[i][j + JN][4 * gq + 1],
-                                          acc[i][j + JN][4 * gq + 2], acc[i][j + JN][4 * gq + 3]);
+            const float4 c1 = *reinterpret_cast<const float4*>(band + r * LDB + BN / 2 + c);
             const float4 h = make_float4(silu_f32(c0.x) * c1.x, silu_f32(c0.y) * c1.y, silu_f32(c0.z) * c1.z,
                                          silu_f32(c0.w) * c1.w);
             if (g.c0) *reinterpret_cast<float4*>((float*)g.c0 + o) = c0;
             if (g.c1) *reinterpret_cast<float4*>((float*)g.c1 + o) = c1;
             *reinterpret_cast<float4*>((float*)g.c2 + o) = h;
           } else if constexpr (KIND == kDownDgrad) {
-            const float4 gi = *reinterpret_cast<const float4*>((const float*)g.x0 + o);
-            const float4 ui = *reinterpret_cast<const float4*>((const float*)g.x1 + o);
-            const float dh[4] = {c0.x, c0.y, c0.z, c0.w}, gv[4] = {gi.x, gi.y, gi.z, gi.w},
-                        uv[4] = {ui.x, ui.y, ui.z, ui.w};
+            const float dh[4] = {c0.x, c0.y, c0.z, c0.w}, gv[4] = {gi[u].x, gi[u].y, gi[u].z, gi[u].w},
+                        uv[4] = {ui[u].x, ui[u].y, ui[u].z, ui[u].w};
             float dg[4], du[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -1160,17 +1190,18 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
             *reinterpret_cast<float4*>((float*)g.c0 + o) = make_float4(dg[0], dg[1], dg[2], dg[3]);
             *reinterpret_cast<float4*>((float*)g.c1 + o) = make_float4(du[0], du[1], du[2], du[3]);
           } else if constexpr (KT::WGRAD) {
-            // expert e's weight gradient; dual-B: fragment j + JN is the up half
+            // expert e's weight gradient; dual-B: the band's second half is the up half
             const int64_t oe = (int64_t)e * g.c_estride + o;
             *reinterpret_cast<float4*>((float*)g.c0 + oe) = c0;
             if constexpr (KT::DUAL_B)
               *reinterpret_cast<float4*>((float*)g.c1 + oe) =
-                  make_float4(acc[i][j + JN][4 * gq], acc[i][j + JN][4 * gq + 1], acc[i][j + JN][4 * gq + 2],
-                              acc[i][j + JN][4 * gq + 3]);
+                  *reinterpret_cast<const float4*>(band + r * LDB + BN / 2 + c);
           } else {
             *reinterpret_cast<float4*>((float*)g.c0 + o) = c0;
           }
         }
+      }
+      if (pb + 1 < BMT / RB) __syncthreads();  // the band is read before the next one overwrites it
     }
     return;
   } else {
