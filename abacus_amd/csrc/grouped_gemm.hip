@@ -688,6 +688,15 @@ __host__ __device__ inline int round_up(int a, int b) { return (a + b - 1) / b *
 
 // Block b of G (a multiple of 8) -> logical tile, XCD-contiguous.
 __device__ inline int xcd_logical(int b, int G) { return (b & 7) * (G >> 3) + (b >> 3); }
+// The same GM x GN groups dealt to the XCDs in turn instead: XCD x takes groups
+// x, x + 8, x + 16, ...  Each expert's groups spread over all XCDs, so experts
+// of unequal row counts (weight-gradient tiles reduce over them) load the XCDs
+// evenly; a launch has a multiple of 8 GM x GN blocks.
+__device__ inline int xcd_dealt(int b) {
+  constexpr int GG = GM * GN;
+  const int j = b >> 3;
+  return ((j / GG) * 8 + (b & 7)) * GG + j % GG;
+}
 
 // Row-grouped kinds (the expert's rows are the output rows): the real row
 // tiles are counted from the offsets, and the real tiles (x tiles_n column
@@ -917,7 +926,10 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     if (part >= 0) slot = r - total / g.split_cus * g.split_cus;
   } else {
     // per-expert tile space (E x tiles_m x tiles_n), XCD-contiguous
-    tl = tile_of_logical(xcd_logical(b, G), g.tiles_m, g.tiles_n);
+    // (fp32: the groups dealt to the XCDs in turn; its blocks are not
+    // persistent, so a contiguous share per XCD would leave the XCDs with
+    // the heavy experts last)
+    tl = tile_of_logical(sizeof(T) == 4 ? xcd_dealt(b) : xcd_logical(b, G), g.tiles_m, g.tiles_n);
   }
   n0 = tl.nt * BNH;
   if (n0 >= g.Ndim) return;
@@ -1797,8 +1809,10 @@ int launch_pipe(const GemmArgs& g, int R, hipStream_t s, const char* name) {
     return launch_rows<T, KIND, -1>(g, R, nullptr, -1, KIND != kDownFwd, s, name);
   } else if constexpr (sizeof(T) == 4) {
     GemmArgs ga = g;
-    const int64_t blocks = pipe_grid<KIND>(ga, R);
-    if (blocks == 0) return 0;
+    const int64_t tiles = pipe_grid<KIND>(ga, R);
+    if (tiles == 0) return 0;
+    // whole turns of groups over the 8 XCDs (xcd_dealt); the extra blocks find no tile
+    const int64_t blocks = (tiles + 8 * pipe::GM * pipe::GN - 1) / (8 * pipe::GM * pipe::GN) * (8 * pipe::GM * pipe::GN);
     ABACUS_CHECK_ARG(blocks < (1ll << 31), "%s: tile grid too large", name);
     hipLaunchKernelGGL((pipe::gemm_tiles_kernel<float, KIND>), dim3((unsigned)blocks), dim3(pipe::NT), 0, s, ga);
     ABACUS_CHECK_LAUNCH(name);
@@ -1888,18 +1902,26 @@ int launch_pipe_pair(const GemmArgs& a, int Ra, const GemmArgs& b, int Rb, hipSt
 // rest).  The routed-row count of a row-grouped kind is free: its tiles clamp
 // their row addresses to the expert's last row.  bf16: every kind.  fp32:
 // the gate/up forward and data gradient, the down projection's forward and
-// the weight gradients (one block per tile), once there is at least one
-// round of 256 x 256 tiles over the CUs (below that the generic kernel's
-// 128 x 128 tiles reach more CUs); the fp32 down-projection data gradient,
-// whose epilogue also reads G and U, measured faster on the generic kernel.
+// the weight gradients (one block per tile, when their tile groups fill
+// evenly), once there is at least one round of 256 x 256 tiles over the CUs
+// (below that the generic kernel's 128 x 128 tiles reach more CUs); the fp32
+// down-projection data gradient, whose epilogue also reads G and U, measured
+// faster on the generic kernel.
 template <int KIND>
 bool pipe_ok(int dtype, const GemmArgs& g, int R) {
   using KT = KindTraits<KIND>;
   if (g.Ndim % 8 != 0 || (KT::WGRAD && g.Mdim % 8 != 0)) return false;
   if (dtype == kBF16) return KT::WGRAD || g.Kdim % pipe::BK == 0;
   constexpr int BNH = KT::DUAL_B ? pipe::BN / 2 : pipe::BN;
-  if (dtype == kF32 && KT::WGRAD)  // one round of per-expert tiles
-    return (int64_t)g.E * ((g.Mdim + pipe::BM - 1) / pipe::BM) * ((g.Ndim + BNH - 1) / BNH) >= cu_count();
+  if (dtype == kF32 && KT::WGRAD) {
+    // one round of per-expert tiles, in GM x GN groups that all hold the
+    // same number of real row tiles (the groups are dealt to the XCDs in
+    // turn, so a mix of full and part-empty groups loads them unevenly:
+    // the down projection's 11 row tiles at M = 2816 measured 9% slower)
+    const int mt = (g.Mdim + pipe::BM - 1) / pipe::BM;
+    if (mt > pipe::GM && mt % pipe::GM != 0) return false;
+    return (int64_t)g.E * mt * ((g.Ndim + BNH - 1) / BNH) >= cu_count();
+  }
   if (dtype != kF32 || KIND == kDownDgrad || g.Kdim % pipe::kBKT<float> != 0) return false;
   return (int64_t)((R + pipe::BM - 1) / pipe::BM) * ((g.Ndim + BNH - 1) / BNH) >= cu_count();
 }
