@@ -273,6 +273,49 @@ def test_fp32_row_products_at_pipelined_sizes():
               f"dX expert {e}")
 
 
+def test_fp32_weight_gradients_at_pipelined_sizes():
+    """fp32 weight gradients with enough per-expert tiles for the pipelined kernel (one block per
+    tile, tile groups dealt to the XCDs in turn): skewed row counts with an empty and a one-row
+    expert, each expert's dW against the fp64 product (relative error 1e-5), exact zeros for the
+    empty expert, and the pair entry points equal to the single ones bit for bit."""
+    counts = [3000, 1, 0, 700, 2500, 129, 1800, 64, 900, 4100, 333, 256, 1200, 40, 2000, 511]
+    D, M = 1024, 1024
+    o = _operands(counts, D, M, torch.float32, seed=43)
+    E, R = o["E"], o["R"]
+    assert E * (M // 256) * (D // 256) >= 256, "a round of down-projection weight-gradient tiles"
+    dev = torch.device("cuda")
+    s = _lib.stream_of(dev)
+    nan = lambda *shape: torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+    dwd, dwg, dwu = nan(E, M, D), nan(E, D, M), nan(E, D, M)
+    call("abacus_moe_down_bwd_wgrad", ptr(o["h"]), ptr(o["dy"]), ptr(o["offsets"]), R, M, D, E, 0, ptr(dwd),
+         ptr(_lib.tile_ctr(dev)), s)
+    call("abacus_moe_gateup_bwd_wgrad", ptr(o["xp"]), ptr(o["dgate"]), ptr(o["dup"]), ptr(o["offsets"]), R, D, M, E,
+         0, ptr(dwg), ptr(dwu), ptr(_lib.tile_ctr(dev)), s)
+    pdg, pdu, pdwd = nan(R, M), nan(R, M), nan(E, M, D)
+    pdx, pdwg, pdwu = nan(R, D), nan(E, D, M), nan(E, D, M)
+    call("abacus_moe_down_bwd", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]), ptr(o["h"]),
+         ptr(o["offsets"]), R, M, D, E, 0, ptr(pdg), ptr(pdu), ptr(pdwd), ptr(_lib.tile_ctr(dev)), s)
+    call("abacus_moe_gateup_bwd", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["xp"]),
+         ptr(o["offsets"]), R, D, M, E, 0, ptr(pdx), ptr(pdwg), ptr(pdwu), ptr(_lib.tile_ctr(dev)), s)
+    torch.cuda.synchronize()
+    for name, a, b in (("dw_down", dwd, pdwd), ("dw_gate", dwg, pdwg), ("dw_up", dwu, pdwu)):
+        assert not torch.isnan(a).any(), f"{name}: unwritten elements"
+        assert torch.equal(a, b), f"{name}: pair and single entry points differ"
+    f = lambda t: t.double()
+    off = o["offsets"].tolist()
+    for e, c in enumerate(counts):
+        a, b = off[e], off[e + 1]
+        if c == 0:
+            for name, t in (("dw_down", dwd), ("dw_gate", dwg), ("dw_up", dwu)):
+                assert torch.count_nonzero(t[e]) == 0, f"{name}: expert {e} without rows"
+            continue
+        for name, got, want in (("dw_down", dwd[e], f(o["h"][a:b]).T @ f(o["dy"][a:b])),
+                                ("dw_gate", dwg[e], f(o["xp"][a:b]).T @ f(o["dgate"][a:b])),
+                                ("dw_up", dwu[e], f(o["xp"][a:b]).T @ f(o["dup"][a:b]))):
+            err = float((f(got) - want).norm() / max(want.norm().item(), 1e-30))
+            assert err < 1e-5, f"{name} expert {e}: relative error {err:.3g}"
+
+
 WGRAD_CASES = [
     # (counts per expert, D, M): fewer tiles than CUs (most blocks find no tile), and more
     ([5, 0, 300, 64], 256, 256),
