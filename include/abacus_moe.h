@@ -101,7 +101,8 @@ int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const v
                           void* gate_RM, void* up_RM, void* h_RM, void* stream);
 
 /* Replaces moe.py:80: y = h @ w_down[e] for every expert.  With a workspace of
- * abacus_moe_down_fwd_ws_bytes bytes (bf16), the tiles beyond the whole rounds
+ * abacus_moe_down_fwd_ws_bytes bytes (bf16, and fp32 batches large enough for
+ * the pipelined kernel), the tiles beyond the whole rounds
  * of the GPU's CUs run as slices of the reduction, whose fp32 partials the
  * workspace holds; ws = NULL (or too small) runs every tile whole.  Either way
  * the same products are summed, in a fixed order: repeated calls agree bit
