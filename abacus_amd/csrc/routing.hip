@@ -82,12 +82,34 @@ __device__ inline uint64_t selection_key(float v, int e) {
   return ((uint64_t)hi << 32) | (uint32_t)~(uint32_t)e;
 }
 
+// One step of row16_max: the larger of v and the v of the lane that DPP
+// control CTRL names (within the same row of 16 lanes).
+template <int CTRL>
+__device__ inline uint64_t dpp_max_step(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xF, 0xF, false);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return o > v ? o : v;
+}
+
+// Maximum of v over each row of 16 lanes, in every lane of the row, by four
+// DPP moves (no LDS): lane i takes the maximum with lane 15 - i (row mirror),
+// then 7 - i within its half (half mirror), 3 - i within its quad, then
+// i ^ 1.  Lane i's set is {i, 15-i}, then {i, 7-i, 8+i, 15-i} for the quad
+// of i, then two such quads, then all 16 lanes.
+__device__ inline uint64_t row16_max(uint64_t v) {
+  v = dpp_max_step<0x140>(v);  // row_mirror
+  v = dpp_max_step<0x141>(v);  // row_half_mirror
+  v = dpp_max_step<0x1B>(v);   // quad_perm [3, 2, 1, 0]
+  return dpp_max_step<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+}
+
 // ---------------------------------------------------------------------------
-// K1: fused router.  One block = 16 tokens x all experts; the NW waves (4, or
-// 16 for batches of at most kRouterWideT tokens) split the D reduction
-// (k-blocks interleaved), partials are summed in LDS in a fixed order, the
-// sigmoid and bias are applied per (token, expert), then 16 lanes per token
-// run the top-k / renormalise epilogue and bump the block's expert histogram.
+// K1: fused router.  One block = 16 tokens x all experts; the NW waves split
+// the D reduction (k-blocks interleaved), partials are summed in LDS in a
+// fixed order, the sigmoid and bias are applied per (token, expert), then 16
+// lanes per token run the top-k / renormalise epilogue and bump the block's
+// expert histogram.
 // ---------------------------------------------------------------------------
 // WLDS (bf16, E a multiple of 8): the weight operand comes from w_DE itself.
 // Each wave loads its k-blocks' rows of w_DE (32 x E, zero-padded to EP
@@ -95,29 +117,49 @@ __device__ inline uint64_t selection_key(float v, int e) {
 // (ds_read_b64_tr_b16), so no transposed copy has to be made first; block 0
 // also writes the transposed rows to wt_out, for the backward.  Otherwise the
 // operand is read from wt, the transposed copy.
-template <typename T, int NF, bool WLDS, int NW>
+//
+// MODE splits the block's work for small batches, where one block streaming
+// all of w_DE is bound by the memory requests one CU keeps in flight:
+//   kRouteFull      the whole kernel as above;
+//   kRoutePart      block (b, s) sums k in [s DS, (s + 1) DS) for token block
+//                   b and stores the fp32 partial logits at part[s][t][EP];
+//   kRouteFromPart  block b adds the kRouterSplit partials of its tokens in
+//                   slice order, then runs the epilogue (no MFMA).
+enum { kRouteFull = 0, kRoutePart = 1, kRouteFromPart = 2 };
+constexpr int kRouterSplit = 8;
+template <typename T, int NF, bool WLDS, int NW, int MODE = kRouteFull>
 __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
     const T* __restrict__ x, const T* __restrict__ wt, const T* __restrict__ w_src, T* __restrict__ wt_out,
     const T* __restrict__ bias, int T_, int D, int E, int K,
     float route_scale, T* __restrict__ logits, T* __restrict__ weights, int64_t* __restrict__ indices,
-    int32_t* __restrict__ idx32, float* __restrict__ score, int32_t* __restrict__ hist) {
+    int32_t* __restrict__ idx32, float* __restrict__ score, int32_t* __restrict__ hist,
+    float* __restrict__ part, int DS) {
   constexpr int VEC = VecTraits<T>::kN;
   constexpr int KB = Mma16<T>::kKB;
   constexpr int EP = NF * 16;
   static_assert(!WLDS || (sizeof(T) == 2 && KB == 32), "the LDS-transposed operand is bf16, 32 k per k-block");
   constexpr int WROW = EP * 2;  // bytes of one staged w row
   constexpr int NTH = NW * 64;
-  __shared__ float red[NW][kRouteTB][EP];
+  constexpr bool MMA = MODE != kRouteFromPart;
+  __shared__ float red[MMA ? NW : 1][kRouteTB][EP];
   __shared__ float s_sc[kRouteTB][EP];
   __shared__ float s_sel[kRouteTB][EP];
   __shared__ int s_cnt[EP];
+  __shared__ float s_bias[EP];
   __shared__ __align__(16) char s_w[WLDS ? NW : 1][WLDS ? 32 * WROW : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int t0 = blockIdx.x * kRouteTB;
-  for (int i = tid; i < EP; i += NTH) s_cnt[i] = 0;
+  // this block's k range: one slice of DS (a multiple of the k-block) or all of D
+  const int kbeg = MODE == kRoutePart ? (int)blockIdx.y * DS : 0;
+  const int kend = MODE == kRoutePart ? min(D, kbeg + DS) : D;
+  for (int i = tid; i < EP; i += NTH) {
+    s_cnt[i] = 0;
+    // read here, used after the first barrier: the load overlaps the logits pass
+    if (MODE != kRoutePart) s_bias[i] = i < E ? to_f32<T>(bias[i]) : 0.f;
+  }
 
   f32x4_t acc[NF];
 #pragma unroll
@@ -130,15 +172,14 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
   const bool vec_ok = (D % VEC) == 0;  // rows are 16-byte aligned only then
   // U k-blocks per batch, all their loads in flight before their MFMAs: one
   // k-block at a time left the pass waiting out a memory latency per k-block.
-  // (16 waves: at most 4, which at D = 2048 is each wave's whole share)
-  constexpr int U = NF <= 2 && NW <= 4 ? 8 : (NF <= 4 ? 4 : (NF <= 8 ? 2 : 1));
+  constexpr int U = NF <= 2 ? 8 : (NF <= 4 ? 4 : (NF <= 8 ? 2 : 1));
   // WLDS: chunk j of this lane in a k-block = w_DE row c / (EP / 8), 8
   // columns at 8 (c % (EP / 8)), c = lane + 64 j (32 rows x EP / 8 chunks).
   auto load_w = [&](int kbu, Vec16* r) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
       const int c = lane + 64 * j, rr = c / (EP / 8), cc = c % (EP / 8);
-      r[j] = (kbu + rr < D && cc * 8 < E) ? ld16(w_src + (int64_t)(kbu + rr) * E + cc * 8) : zero16();
+      r[j] = (kbu + rr < kend && cc * 8 < E) ? ld16(w_src + (int64_t)(kbu + rr) * E + cc * 8) : zero16();
     }
   };
   // WLDS: stage a k-block's chunks in this wave's buffer, read the NF
@@ -169,18 +210,22 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
       bf[f].w[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
       bf[f].w[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
       bf[f].w[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
-      if (wt_out != nullptr && blockIdx.x == 0 && kbu + 8 * grp < D)
+      if (wt_out != nullptr && blockIdx.x == 0 && kbu + 8 * grp < kend)
         st16(wt_out + (int64_t)(f * 16 + s) * D + kbu + 8 * grp, bf[f]);
     }
   };
-  int kb0 = wave * KB;
-  if (vec_ok) {
-    for (; kb0 + (U - 1) * NW * KB < D; kb0 += U * NW * KB) {
+  int kb0 = kbeg + wave * KB;
+  // Batches of U k-blocks.  A slice runs its last batch partly past kend
+  // (loads of zeros), so all of a wave's slice is one batch in flight; the
+  // whole-D pass leaves such a remainder to the single-k-block loop below.
+  const int kb_lim = MODE == kRoutePart ? kend : kend - (U - 1) * NW * KB;
+  if (vec_ok && MMA) {
+    for (; kb0 < kb_lim; kb0 += U * NW * KB) {
       Vec16 a[U], b[U][NF];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int k = kb0 + u * NW * KB + kg;
-        const bool k_ok = k < D;
+        const bool k_ok = k < kend;
         a[u] = (row_ok && k_ok) ? ld16(xrow + k) : zero16();
         if constexpr (WLDS) {
           load_w(kb0 + u * NW * KB, b[u]);
@@ -204,7 +249,7 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
       }
     }
   }
-  for (int kb = kb0; kb < D; kb += NW * KB) {
+  for (int kb = kb0; MMA && kb < kend; kb += NW * KB) {
     const int k = kb + kg;
     Vec16 a, b[NF];
     if constexpr (WLDS) {  // vec_ok holds on this path
@@ -235,36 +280,70 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
     for (int f = 0; f < NF; ++f) Mma16<T>::run(acc[f], a, b[f]);
   }
   // acc[f][r] = partial logit of token 4*(lane/16)+r, expert f*16 + lane%16
+  if constexpr (MMA) {
 #pragma unroll
-  for (int f = 0; f < NF; ++f)
+    for (int f = 0; f < NF; ++f)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[wave][4 * (lane >> 4) + r][f * 16 + (lane & 15)] = acc[f][r];
+      for (int r = 0; r < 4; ++r) red[MMA ? wave : 0][4 * (lane >> 4) + r][f * 16 + (lane & 15)] = acc[f][r];
+  } else {
+    // every partial of this thread's (token, expert) pairs in flight at once,
+    // then their sums in slice order (so independent of block timing) to red[0]
+    constexpr int PER = (kRouteTB * EP + NTH - 1) / NTH;
+    float p[PER][kRouterSplit];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid + j * NTH, t = t0 + i / EP;
+      const bool ok = i < kRouteTB * EP && t < T_;
+#pragma unroll
+      for (int s = 0; s < kRouterSplit; ++s) p[j][s] = ok ? part[((int64_t)s * T_ + t) * EP + i % EP] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = tid + j * NTH;
+      float l = p[j][0];
+#pragma unroll
+      for (int s = 1; s < kRouterSplit; ++s) l += p[j][s];
+      if (i < kRouteTB * EP) red[0][i / EP][i % EP] = l;
+    }
+  }
   __syncthreads();
 
   for (int i = tid; i < kRouteTB * EP; i += NTH) {
     const int tok = i / EP, e = i % EP;
-    float l = red[0][tok][e];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) l += red[w][tok][e];
     const int t = t0 + tok;
+    float l = 0.f;
+    if constexpr (MODE == kRouteFromPart) {
+      l = red[0][tok][e];
+    } else {
+      l = red[0][tok][e];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) l += red[MMA ? w : 0][tok][e];
+    }
+    if constexpr (MODE == kRoutePart) {
+      if (t < T_) part[((int64_t)blockIdx.y * T_ + t) * EP + e] = l;
+      continue;
+    }
     if (e < E && t < T_) {
       const float lr = round_to<T>(l);
       logits[(int64_t)t * E + e] = from_f32<T>(lr);
       const float s = round_to<T>(sigmoid_f32_cr(lr));
       s_sc[tok][e] = s;
-      s_sel[tok][e] = round_to<T>(s + to_f32<T>(bias[e]));
+      s_sel[tok][e] = round_to<T>(s + s_bias[e]);
     }
   }
+  if constexpr (MODE == kRoutePart) return;
   __syncthreads();
 
   // Top-K: L lanes per token, lane j of a token holding experts j, j + L, ...
   // as selection keys.  Each of the K rounds takes the maximum key over the
-  // token's lanes (a local maximum, then log2(L) butterfly steps) and retires
-  // that expert.  The rounds are a chain of dependent lane shuffles, so up to
-  // 64 experts a token gets 16 lanes (4 tokens per wave at once, a block's 16
-  // tokens in one pass; with 64 lanes, 6 steps and a token per pass, this
-  // epilogue took most of the kernel's ~28 us at small batches); beyond 64
-  // experts, 64 lanes keep the keys per lane (and registers) few.
+  // token's lanes (a local maximum, then the row-of-16 maximum by DPP moves,
+  // and for L = 64 two lane shuffles) and retires that expert; the picks'
+  // scores are read and summed after the rounds.  The rounds are a chain of
+  // dependent steps, so up to 64 experts a token gets 16 lanes (4 tokens per
+  // wave at once, a block's 16 tokens in one pass; with 64 lanes and a token
+  // per pass this epilogue took most of the kernel's ~28 us at small
+  // batches); beyond 64 experts, 64 lanes keep the keys per lane (and
+  // registers) few.
   constexpr int L = EP <= 64 ? 16 : 64;
   constexpr int TPW = 64 / L;                  // tokens per wave pass
   constexpr int CPL = EP <= L ? 1 : EP / L;    // experts per lane
@@ -279,32 +358,33 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
       const int e = ln + L * c;
       key[c] = valid && e < E ? selection_key(s_sel[tok][e], e) : 0ull;
     }
-    float sum = 0.f, my_s = 0.f;
-    int my_e = 0;
+    int my_e = 0;  // lane k: the k-th pick
     for (int k = 0; k < K; ++k) {
       uint64_t best = key[0];
 #pragma unroll
       for (int c = 1; c < CPL; ++c) best = key[c] > best ? key[c] : best;
+      best = row16_max(best);
+      if constexpr (L == 64) {
 #pragma unroll
-      for (int off = L / 2; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)best, off, L);
-        const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, L);
-        const uint64_t o = ((uint64_t)hi << 32) | lo;
-        best = o > best ? o : best;
+        for (int off = 16; off < 64; off <<= 1) {
+          const uint32_t lo = __shfl_xor((uint32_t)best, off, 64);
+          const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64);
+          const uint64_t o = ((uint64_t)hi << 32) | lo;
+          best = o > best ? o : best;
+        }
       }
       const int be = valid ? (int)(~(uint32_t)best) : 0;
 #pragma unroll
       for (int c = 0; c < CPL; ++c)
         if (ln + L * c == be) key[c] = 0ull;
-      const float sc = s_sc[tok][be];
-      sum += sc;  // pick order
-      if (ln == k) {
-        my_s = sc;
-        my_e = be;
-      }
-      if (valid && ln == 0) atomicAdd(&s_cnt[be], 1);
+      if (ln == k) my_e = be;
     }
+    // (lanes past K, and invalid tokens, read a score they do not use)
+    const float my_s = s_sc[tok][my_e];
+    float sum = 0.f;
+    for (int k = 0; k < K; ++k) sum += __shfl(my_s, k, L);  // pick order
     if (valid && ln < K) {
+      atomicAdd(&s_cnt[my_e], 1);
       const float denom = round_to<T>(sum);
       const float w = round_to<T>(round_to<T>(my_s / denom) * route_scale);
       const int64_t o = (int64_t)t * K + ln;
@@ -446,9 +526,44 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
   const int t0 = blockIdx.x * kRouteTB;
   const bool writer = blockIdx.y == 0;
   const int ntok = min(kRouteTB, T_ - t0);
+  // Loads that need no routing go first and are in flight during the scan:
+  // this block's slots and its first batch of x vectors (tokens t0.., columns
+  // c0 .. c0 + ncol of this block's chunk).
+  int my_e = -1;
+  if (tid < kRouteTB * K && tid / K < ntok) my_e = idx[(int64_t)t0 * K + tid];
+  const int nvec = D / VEC;
+  const int per = (nvec + gridDim.y - 1) / gridDim.y;  // columns of this chunk
+  const int c0 = blockIdx.y * per;
+  const int ncol = max(0, min(nvec, c0 + per) - c0);
+  const int total = ntok * ncol;
+  Vec16 v[U];
+  int tok[U], col[U];
+  auto load_batch = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * 256 + tid;
+      tok[u] = i / ncol;
+      col[u] = c0 + i % ncol;
+      if (i < total) v[u] = ld16(x + (int64_t)(t0 + tok[u]) * D + (int64_t)col[u] * VEC);
+    }
+  };
+  if (total > 0) load_batch(0);
   if constexpr (SCAN) {
     const int nb = (int)gridDim.x, lane = tid & 63, q = tid >> 6;
-    for (int i = tid; i < nb * E; i += 256) s_h[i] = hist[i];
+    // the histograms to LDS, 8 loads per thread in flight (nb * E <= kFusedScanInts)
+    for (int i0 = 0; i0 < nb * E; i0 += 256 * 8) {
+      int h[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + u * 256 + tid;
+        h[u] = i < nb * E ? hist[i] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + u * 256 + tid;
+        if (i < nb * E) s_h[i] = h[u];
+      }
+    }
     __syncthreads();
     // thread t: expert t % E over blocks t / E, t / E + NP, ... (NP = 256 / E parts), all of
     // them and those before this block; then thread e adds its expert's NP parts
@@ -499,10 +614,7 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     }
     __syncthreads();
   }
-  if (tid < kRouteTB * K) {
-    const int tok = tid / K, k = tid % K;
-    s_e[tok][k] = tok < ntok ? idx[(int64_t)(t0 + tok) * K + k] : -1;
-  }
+  if (tid < kRouteTB * K) s_e[tid / K][tid % K] = my_e;
   __syncthreads();
   if (tid < ntok * K) {
     const int tok = tid / K, k = tid % K;
@@ -518,21 +630,8 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     s_pos[tok][k] = p;
   }
   __syncthreads();
-  const int nvec = D / VEC;
-  const int per = (nvec + gridDim.y - 1) / gridDim.y;  // columns of this chunk
-  const int c0 = blockIdx.y * per;
-  const int ncol = max(0, min(nvec, c0 + per) - c0);
-  const int total = ntok * ncol;
   for (int i0 = 0; i0 < total; i0 += 256 * U) {
-    Vec16 v[U];
-    int tok[U], col[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * 256 + tid;
-      tok[u] = i / ncol;
-      col[u] = c0 + i % ncol;
-      if (i < total) v[u] = ld16(x + (int64_t)(t0 + tok[u]) * D + (int64_t)col[u] * VEC);
-    }
+    if (i0 > 0) load_batch(i0);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = i0 + u * 256 + tid;
@@ -635,8 +734,9 @@ constexpr int kGatherBatch = 4;
 // Batches of at most this many tokens combine in column chunks (a wave per
 // token and 64-vector chunk, every slot's loads in flight at once).
 constexpr int64_t kCombineSmallT = 1024;
-// Batches of at most this many tokens run the router with 16 waves per block.
-constexpr int64_t kRouterWideT = 1024;
+// Batches of at most this many tokens run the bf16 router (E <= 64) as
+// kRouterSplit slices of D and a second pass over the partial logits.
+constexpr int64_t kRouterSplitT = 1024;
 
 // ---------------------------------------------------------------------------
 // K6: combine.  out[t] = sum_k round(y[pos(t,k)] * w(t,k)), experts ascending,
@@ -1382,6 +1482,14 @@ inline int e_pad(int64_t E) {
   return p <= 64 ? p : (p <= 128 ? 128 : 256);
 }
 
+// The router workspace: the transposed weight (e_pad(E), D), then, for the
+// split router, the fp32 partial logits (kRouterSplit, T, e_pad(E)) of up to
+// kRouterSplitT tokens.
+inline int64_t router_part_offset(int64_t D, int64_t E, int dtype) {
+  return ((int64_t)e_pad(E) * D * elem_size(dtype) + 255) / 256 * 256;
+}
+inline int64_t router_part_bytes(int64_t E) { return (int64_t)kRouterSplit * kRouterSplitT * e_pad(E) * 4; }
+
 // The allocation-free router weight gradient's partial sums: a static device
 // array, one copy per GPU, held until the process ends.  Host code must never
 // pass `scratch` itself to a kernel (its host-side name is only a handle):
@@ -1416,6 +1524,14 @@ float* scratch_ptr() {
   return g_scratch_dev[dev];
 }
 
+// Column chunks of the gather: enough of them for ~1024 blocks, each at least
+// 16 vectors wide.  A small batch thus spreads its rows over many CUs (one CU
+// moves only the bytes its requests in flight allow), a large one keeps
+// whole rows in a block.
+inline unsigned gather_ysplit(int64_t nb, int64_t nvec) {
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(nvec / 16, (1024 + nb - 1) / nb));
+}
+
 // Calls f(std::integral_constant<int, KB>) with KB = K rounded up to 1, 2, 4,
 // 8 or 16: the slot bound of the wave-per-token gather kernels.
 template <typename F>
@@ -1434,7 +1550,7 @@ extern "C" {
 int64_t abacus_moe_hist_len(int64_t T, int64_t E) { return ((T + kRouteTB - 1) / kRouteTB) * E; }
 
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype) {
-  return (int64_t)e_pad(E) * D * elem_size(dtype);
+  return router_part_offset(D, E, dtype) + (dtype == kBF16 && e_pad(E) <= 64 ? router_part_bytes(E) : 0);
 }
 
 int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
@@ -1455,28 +1571,33 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   }
   if (nb == 0) return 0;
   if (wlds) {
-#define ROUTER_LAUNCH_W(NF, NW)                                                                                      \
-  hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true, NW>), dim3(nb), dim3(NW * 64), 0, s,                      \
-                     (const uint16_t*)x_TD, (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws,        \
-                     (const uint16_t*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE,      \
-                     (uint16_t*)weights_TK, indices_TK, idx_TK, score_TK, hist)
-    // small batches: 16 waves per block split D four times finer, so each
-    // wave's loads are one batch in flight instead of a chain of batches
-    if (T <= kRouterWideT) {
-      switch (EP / 16) {
-        case 1: ROUTER_LAUNCH_W(1, 16); break;
-        case 2: ROUTER_LAUNCH_W(2, 16); break;
-        case 3: ROUTER_LAUNCH_W(3, 16); break;
-        default: ROUTER_LAUNCH_W(4, 16); break;
-      }
+#define ROUTER_LAUNCH_W(NF, MODE, GRID)                                                                              \
+  hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true, 4, MODE>), GRID, dim3(256), 0, s, (const uint16_t*)x_TD, \
+                     (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws, (const uint16_t*)bias_E,      \
+                     (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE, (uint16_t*)weights_TK,        \
+                     indices_TK, idx_TK, score_TK, hist, part, DS)
+#define ROUTER_SWITCH_NF(MODE, GRID)            \
+  switch (EP / 16) {                            \
+    case 1: ROUTER_LAUNCH_W(1, MODE, GRID); break; \
+    case 2: ROUTER_LAUNCH_W(2, MODE, GRID); break; \
+    case 3: ROUTER_LAUNCH_W(3, MODE, GRID); break; \
+    default: ROUTER_LAUNCH_W(4, MODE, GRID); break; \
+  }
+    // Small batches: a block per token block streams all of w_DE through one
+    // CU, bound by the requests a CU keeps in flight; kRouterSplit slices of
+    // D spread that over kRouterSplit times the blocks, and a second pass
+    // adds the slices in order and routes.
+    float* part = reinterpret_cast<float*>(static_cast<char*>(wt_ws) + router_part_offset(D, E, dtype));
+    const int nkb = (int)((D + 31) / 32);
+    const int DS = 32 * ((nkb + kRouterSplit - 1) / kRouterSplit);
+    if (T <= kRouterSplitT) {
+      ROUTER_SWITCH_NF(kRoutePart, dim3(nb, kRouterSplit))
+      ABACUS_CHECK_LAUNCH("router_fwd (slices)");
+      ROUTER_SWITCH_NF(kRouteFromPart, dim3(nb))
     } else {
-      switch (EP / 16) {
-        case 1: ROUTER_LAUNCH_W(1, 4); break;
-        case 2: ROUTER_LAUNCH_W(2, 4); break;
-        case 3: ROUTER_LAUNCH_W(3, 4); break;
-        default: ROUTER_LAUNCH_W(4, 4); break;
-      }
+      ROUTER_SWITCH_NF(kRouteFull, dim3(nb))
     }
+#undef ROUTER_SWITCH_NF
 #undef ROUTER_LAUNCH_W
     ABACUS_CHECK_LAUNCH("router_fwd");
     return 0;
@@ -1484,7 +1605,8 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
 #define ROUTER_LAUNCH(TT, NF)                                                                                      \
   hipLaunchKernelGGL((router_fwd_kernel<TT, NF, false, 4>), dim3(nb), dim3(256), 0, s, (const TT*)x_TD,           \
                      (const TT*)wt_ws, (const TT*)nullptr, (TT*)nullptr, (const TT*)bias_E, (int)T, (int)D, (int)E, \
-                     (int)K, route_scale, (TT*)logits_TE, (TT*)weights_TK, indices_TK, idx_TK, score_TK, hist)
+                     (int)K, route_scale, (TT*)logits_TE, (TT*)weights_TK, indices_TK, idx_TK, score_TK, hist,  \
+                     nullptr, 0)
 #define ROUTER_DISPATCH_NF(TT)          \
   switch (EP / 16) {                    \
     case 1: ROUTER_LAUNCH(TT, 1); break; \
@@ -1537,10 +1659,7 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
   if (nb == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
-  // column chunks of at least 64 vectors, enough of them for ~1024 blocks
-  const int64_t nvec = D / vec_elems(dtype);
-  const unsigned ysplit = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nvec / 64, (1024 + nb - 1) / nb));
-  const dim3 grid((unsigned)nb, ysplit);
+  const dim3 grid((unsigned)nb, gather_ysplit(nb, D / vec_elems(dtype)));
   if (dtype == kBF16)
     hipLaunchKernelGGL((permute_gather_kernel<uint16_t, false>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
                        base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, nullptr, nullptr,
@@ -1568,9 +1687,7 @@ int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* id
     return abacus_moe_route_scan(hist, T, E, K, bias_E, bias_update_speed, dtype, base_ws, counts_E, offsets_E1,
                                  stream);
   hipStream_t s = (hipStream_t)stream;
-  const int64_t nvec = D / vec_elems(dtype);
-  const unsigned ysplit = (unsigned)std::max<int64_t>(1, std::min<int64_t>(nvec / 64, (1024 + nb - 1) / nb));
-  const dim3 grid((unsigned)nb, ysplit);
+  const dim3 grid((unsigned)nb, gather_ysplit(nb, D / vec_elems(dtype)));
   if (dtype == kBF16)
     hipLaunchKernelGGL((permute_gather_kernel<uint16_t, true>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
                        nullptr, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, hist,

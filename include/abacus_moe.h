@@ -45,7 +45,9 @@ const char* abacus_moe_last_error(void);
 int abacus_moe_abi_version(void);
 /* int32 elements of the per-token-block expert histogram (and of `base`). */
 int64_t abacus_moe_hist_len(int64_t T, int64_t E);
-/* bytes of the transposed router-weight scratch used by router_fwd / unpermute_bwd. */
+/* bytes of the router workspace used by router_fwd / unpermute_bwd: the
+ * transposed router weight and, for bf16 with E <= 64, room for the partial
+ * logits of router_fwd's split small-batch pass (T <= 1024); independent of T. */
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
 /* bytes of the fp32 partial-sum scratch used by router_wgrad. */
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E);

@@ -123,6 +123,83 @@ def test_router_backward_matches_oracle(dtype):
         torch.testing.assert_close(got.float().cpu(), want, rtol=tol, atol=tol * float(want.pow(2).mean().sqrt()))
 
 
+@pytest.mark.parametrize("T,D,E,K", [(1, 64, 8, 2), (16, 4096, 32, 2), (700, 2048, 48, 4), (1024, 264, 64, 6),
+                                     (1025, 264, 64, 6)])
+def test_router_small_batch_slices(T, D, E, K):
+    """bf16 routers with at most 64 experts and at most 1024 tokens sum the logits over 8 slices of D
+    in a second launch (at D = 264 the last three slices are empty; 1025 tokens take the one-launch
+    path).  Through the C ABI: the transposed weight the slice blocks write into the workspace is
+    exactly w_DE^T (zero rows past E) and the block histograms count the picks.  Through the module:
+    routing bit-exact against the oracle given the kernel's logits, logits close to an fp32
+    product, input and weight gradients close to fp64 (xavier-initialised weights, logits O(1))."""
+    from abacus_amd._lib import call, ptr, query, stream_of, dtype_code
+    print(f"\n[router-slices] T={T} D={D} E={E} K={K}", flush=True)
+    gen = torch.Generator().manual_seed(T * 7 + D)
+    router = Router(D, E, K, route_scale=1.5).to(device=DEV, dtype=torch.bfloat16)
+    bias0 = (torch.randn(E, generator=gen) * 0.1).to(torch.bfloat16)
+    with torch.no_grad():
+        router.expert_bias_E.copy_(bias0)
+    x = torch.randn(T, D, generator=gen).to(device=DEV, dtype=torch.bfloat16)
+    w_DE = router.w_DE.detach()
+
+    dt, st = dtype_code(torch.bfloat16), stream_of(DEV)
+    EP = (E + 15) // 16 * 16
+    logits = torch.empty(T, E, dtype=torch.bfloat16, device=DEV)
+    weights = torch.empty(T, K, dtype=torch.bfloat16, device=DEV)
+    ind = torch.empty(T, K, dtype=torch.int64, device=DEV)
+    idx32 = torch.empty(T, K, dtype=torch.int32, device=DEV)
+    score = torch.empty(T, K, dtype=torch.float32, device=DEV)
+    hist = torch.full((query("abacus_moe_hist_len", T, E),), -1, dtype=torch.int32, device=DEV)
+    ws = torch.full((query("abacus_moe_router_ws_bytes", D, E, dt),), 0x7F, dtype=torch.uint8, device=DEV)
+    call("abacus_moe_router_fwd", ptr(x), ptr(w_DE), ptr(router.expert_bias_E), T, D, E, K, 1.5, dt, ptr(logits),
+         ptr(weights), ptr(ind), ptr(idx32), ptr(score), ptr(hist), ptr(ws), st)
+    torch.cuda.synchronize()
+    wt = ws[: EP * D * 2].view(torch.bfloat16).reshape(EP, D).cpu()
+    want = torch.zeros(EP, D, dtype=torch.bfloat16)
+    want[:E] = w_DE.t().cpu()
+    assert torch.equal(wt, want)
+    nb = (T + 15) // 16
+    h = torch.zeros(nb, E, dtype=torch.int32)
+    for t, row in enumerate(ind.cpu().tolist()):
+        for e in row:
+            h[t // 16, e] += 1
+    assert torch.equal(hist.cpu().reshape(nb, E), h)
+
+    xg = x.clone().requires_grad_()
+    router.eval()
+    w, idx = router(xg)
+    torch.cuda.synchronize()
+    lg = router.last_routing.logits_TE.cpu()
+    assert torch.equal(lg, logits.cpu()) and torch.equal(idx, ind)
+    w_o, idx_o, _ = oracle.route(lg, bias0, K, router.route_scale)
+    assert torch.equal(idx.cpu(), idx_o)
+    assert torch.equal(w.detach().cpu(), w_o)
+    ref = (x.float() @ w_DE.float()).cpu()
+    torch.testing.assert_close(lg.float(), ref, rtol=1e-2, atol=1e-2 * float(ref.std()))
+
+    # Gradients against fp64 products with the kernel's own gating quantities (bf16 scores,
+    # weights and rounded score sum in the formula of router.py:45,49-51: dL/dlogit_j =
+    # (rho dw_j - sum_k dw_k w_k) / S * s_j (1 - s_j)), so the check is on the products with
+    # w_DE (through the transposed copy) and x, not on bf16 rounding of saturated sigmoids.
+    g = torch.randn(T, K, generator=gen)
+    (w.float() * g.to(DEV)).sum().backward()
+    sc, wk = score.cpu().double(), weights.cpu().double()
+    dwk = g.to(torch.bfloat16).double()
+    S = sc.sum(-1, keepdim=True).to(torch.bfloat16).double()
+    dl = (1.5 * dwk - (dwk * wk).sum(-1, keepdim=True)) / S * sc * (1 - sc)
+    G = torch.zeros(T, E, dtype=torch.float64).scatter_add_(1, ind.cpu(), dl)
+    dx_ref = (G @ w_DE.cpu().double().t()).float()
+    torch.testing.assert_close(xg.grad.float().cpu(), dx_ref, rtol=1e-2, atol=1e-2 * float(dx_ref.pow(2).mean().sqrt()))
+    # dW = x^T G takes G as a bf16 operand (as bf16 autograd holds dlogits) and rounds once: per
+    # element within 2^-9 of |x|^T |G| plus 2^-9 of the value, each allowed twice (where two
+    # tokens' terms cancel, the operand rounding exceeds any tolerance relative to the value)
+    xa = x.cpu().double()
+    dw_ref = xa.t() @ G
+    bound = 2.0**-8 * (xa.abs().t() @ G.abs() + dw_ref.abs())
+    err = (router.w_DE.grad.double().cpu() - dw_ref).abs()
+    assert bool((err <= bound).all()), float((err - bound).max())
+
+
 def test_update_bias_explicit_indices():
     router = Router(4, 4, 2, bias_update_speed=0.5).to(DEV)
     idx = torch.tensor([[0, 1], [0, 2], [0, 1]], device=DEV)
