@@ -22,6 +22,7 @@
 // v_mfma_f32_16x16x4_f32; accumulation is always fp32.
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "common.h"
 
@@ -995,6 +996,8 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     else sb.template issue_one<KT::WGRAD>(n - DMA_A, dma_stage + A_BYTES, wave_u, dma_k0, k_len);
   };
 
+  // rows of this wave's part of the tile that hold data (wave-uniform)
+  const int wave_rows = __builtin_amdgcn_readfirstlane(row_end - row0 - wm * WTM);
   typename Op::Acc acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -1037,14 +1040,18 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // fenced with sched_barrier so the interleave survives scheduling: with one
   // wave per SIMD, nothing else keeps the matrix core busy while this wave
   // waits on LDS or issues loads.
-  auto kstep = [&](int slot, bool with_read, const char* rd_st, int rd_t, int rd_slot, bool with_dma) __attribute__((always_inline)) {
+  //
+  // LF (a compile-time count, lfc) is how many of the wave's FM row fragments
+  // get MFMAs: the rest lie wholly past the tile's rows and are never stored.
+  auto kstep = [&](auto lfc, int slot, bool with_read, const char* rd_st, int rd_t, int rd_slot, bool with_dma) __attribute__((always_inline)) {
+    constexpr int LF = decltype(lfc)::value;
     constexpr int MF = FM * FN;
     static_assert(MF >= NFRAG, "one fragment read per MFMA at most");
 #pragma unroll
     for (int m = 0; m < MF; ++m) {
       // operands swapped: the fragment is C^T, so each lane ends up holding
       // runs of 4 consecutive columns of one row (see the epilogue)
-      Op::run(acc[m / FN][m % FN], bfr[slot][m % FN], af[slot][m / FN]);
+      if (m / FN < LF) Op::run(acc[m / FN][m % FN], bfr[slot][m % FN], af[slot][m / FN]);
       if (with_read && m < NFRAG) read_frag(rd_st, rd_t, rd_slot, m);
       if (with_dma) {
 #pragma unroll
@@ -1068,18 +1075,18 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
   // tile kt+1 land (so that tile can be read).  The last step's MFMAs then
   // cover the first reads of tile kt+1 and the DMA of tile kt+ST into
   // this stage.
-  auto ktile = [&](int kt, bool next, bool dma_next) __attribute__((always_inline)) {
+  auto ktile = [&](auto lfc, int kt, bool next, bool dma_next) __attribute__((always_inline)) {
     char* st = lds + (kt % ST) * STAGE_BYTES;
     char* st_next = lds + ((kt + 1) % ST) * STAGE_BYTES;
 #pragma unroll
-    for (int t = 0; t < NSTEP - 1; ++t) kstep(t & 1, true, st, t + 1, (t + 1) & 1, false);
+    for (int t = 0; t < NSTEP - 1; ++t) kstep(lfc, t & 1, true, st, t + 1, (t + 1) & 1, false);
     // tiles kt+2 .. min(kt+ST-1, ktiles-1) may still be in flight
     wait_next(min(ST - 2, ktiles - 2 - kt));
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's reads of the stage are back
     __syncthreads();
     if (dma_next) prep(kt + ST);
     __builtin_amdgcn_sched_barrier(0);
-    kstep((NSTEP - 1) & 1, next, st_next, 0, 0, dma_next);
+    kstep(lfc, (NSTEP - 1) & 1, next, st_next, 0, 0, dma_next);
   };
 
   // prologue: tiles 0 .. ST-1 in flight, tile 0's first fragments read.
@@ -1106,10 +1113,16 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmArgs& 
     for (int f = 0; f < NFRAG; ++f) read_frag(lds, 0, 0, f);
 
     // steady state, then the last tiles (no DMA; no next tile for the last)
-    int kt = 0;
-    for (; kt + ST < ktiles; ++kt) ktile(kt, true, true);
-    for (; kt + 1 < ktiles; ++kt) ktile(kt, true, false);
-    ktile(kt, false, false);
+    auto run_tiles = [&](auto lfc) __attribute__((always_inline)) {
+      int kt = 0;
+      for (; kt + ST < ktiles; ++kt) ktile(lfc, kt, true, true);
+      for (; kt + 1 < ktiles; ++kt) ktile(lfc, kt, true, false);
+      ktile(lfc, kt, false, false);
+    };
+    // a small batch fills one row fragment of a thin tile, or none of a wave's
+    if (wave_rows > 32 || FM == 1) run_tiles(std::integral_constant<int, FM>());
+    else if (wave_rows > 0) run_tiles(std::integral_constant<int, 1>());
+    else run_tiles(std::integral_constant<int, 0>());
   }
   if (part >= 0) {
     // a slice of a split tile: its fp32 partial, row-major, for split_reduce_kernel
