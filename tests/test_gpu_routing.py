@@ -217,11 +217,14 @@ def test_selection_order_special_values(E, K, dtype):
 
 @pytest.mark.parametrize("T,D,E,K,dtype", [(1, 64, 4, 2, torch.float32), (200, 128, 64, 6, torch.bfloat16),
                                            (4096, 256, 8, 2, torch.bfloat16), (3000, 64, 16, 4, torch.float32),
-                                           (5000, 64, 16, 2, torch.bfloat16), (33, 72, 256, 16, torch.bfloat16)])
+                                           (5000, 64, 16, 2, torch.bfloat16), (33, 72, 256, 16, torch.bfloat16),
+                                           (64, 328, 64, 6, torch.bfloat16), (48, 1032, 16, 4, torch.float32),
+                                           (64, 2048, 64, 6, torch.bfloat16)])
 def test_dispatch_matches_scan_then_gather(T, D, E, K, dtype):
     """abacus_moe_dispatch (one launch when the block histograms hold at most 4096 ints: the gather
     blocks scan them) equals abacus_moe_route_scan + abacus_moe_permute_gather bit for bit:
-    counts, offsets, pos, perm, the gathered rows and the bias step."""
+    counts, offsets, pos, perm, the gathered rows and the bias step; counts, perm and the gathered
+    rows (x[perm]) equal the oracle's."""
     from abacus_amd._lib import call, ptr, query, stream_of, dtype_code
     print(f"\n[dispatch] T={T} D={D} E={E} K={K} {dtype}", flush=True)
     gen = torch.Generator().manual_seed(T + E)
@@ -265,3 +268,6 @@ def test_dispatch_matches_scan_then_gather(T, D, E, K, dtype):
         assert torch.equal(a, b), name
     counts_o, offsets_o, perm_o, pos_o = oracle.dispatch(idx.cpu().long(), E)
     assert outs[1][0].tolist() == counts_o.tolist() and outs[1][3].tolist() == perm_o.tolist()
+    # the gathered rows themselves: small batches split each row over column chunks (at D = 328 bf16,
+    # 41 vectors in 2 uneven chunks; at D = 1032 fp32, 258 vectors in 16 chunks, the last of 3)
+    assert torch.equal(outs[1][4], x.cpu()[torch.as_tensor(perm_o, dtype=torch.long)])
