@@ -420,7 +420,7 @@ void router_wgrad(const T* x, const float* dlogit, const int32_t* idx, int64_t T
 extern "C" {
 
 const char* abacus_moe_last_error(void) { return g_error; }
-int abacus_moe_abi_version(void) { return 2; }
+int abacus_moe_abi_version(void) { return 3; }
 
 int64_t abacus_moe_hist_len(int64_t T, int64_t E) { return ((T + kTokBlock - 1) / kTokBlock) * E; }
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype) { return (int64_t)e_pad(E) * D * elem(dtype); }

@@ -42,6 +42,8 @@ enum { ABACUS_F32 = 0, ABACUS_BF16 = 1 };
 
 /* ---- library / sizing queries ------------------------------------------ */
 const char* abacus_moe_last_error(void);
+/* 3: abacus_moe_router_ws_bytes also covers the small-batch router's partial
+ * logits (size the workspace by the query, never by a formula). */
 int abacus_moe_abi_version(void);
 /* int32 elements of the per-token-block expert histogram (and of `base`). */
 int64_t abacus_moe_hist_len(int64_t T, int64_t E);
