@@ -515,9 +515,10 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
                                                              int32_t* __restrict__ offsets) {
   constexpr int VEC = VecTraits<T>::kN;
   constexpr int U = kPermuteBatch;
-  static_assert(kRouteTB * kMaxK <= 256, "one thread per (token, slot) pair");
+  static_assert(kRouteTB * kMaxK == 256, "one thread per (token, slot) entry of s_e");
   static_assert(kMaxE == 256, "one thread per expert in the scan");
-  __shared__ int s_e[kRouteTB][kMaxK];
+  static_assert(kMaxK % 4 == 0, "a token's slots as 16-byte vectors");
+  __shared__ __align__(16) int s_e[kRouteTB][kMaxK];  // -1 past K and past the batch
   __shared__ int s_pos[kRouteTB][kMaxK];
   __shared__ int s_h[SCAN ? kFusedScanInts : 1];
   __shared__ int s_all[SCAN ? 256 : 1], s_prev[SCAN ? 256 : 1], s_base[SCAN ? kMaxE : 1];
@@ -527,10 +528,11 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
   const bool writer = blockIdx.y == 0;
   const int ntok = min(kRouteTB, T_ - t0);
   // Loads that need no routing go first and are in flight during the scan:
-  // this block's slots and its first batch of x vectors (tokens t0.., columns
-  // c0 .. c0 + ncol of this block's chunk).
+  // this block's slots (thread t: token t / kMaxK, slot t % kMaxK) and its
+  // first batch of x vectors (tokens t0.., columns c0 .. c0 + ncol of this
+  // block's chunk).
   int my_e = -1;
-  if (tid < kRouteTB * K && tid / K < ntok) my_e = idx[(int64_t)t0 * K + tid];
+  if (tid % kMaxK < K && tid / kMaxK < ntok) my_e = idx[(int64_t)(t0 + tid / kMaxK) * K + tid % kMaxK];
   const int nvec = D / VEC;
   const int per = (nvec + gridDim.y - 1) / gridDim.y;  // columns of this chunk
   const int c0 = blockIdx.y * per;
@@ -614,14 +616,27 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     }
     __syncthreads();
   }
-  if (tid < kRouteTB * K) s_e[tid / K][tid % K] = my_e;
+  if (tid < kRouteTB * kMaxK) s_e[tid / kMaxK][tid % kMaxK] = my_e;
   __syncthreads();
   if (tid < ntok * K) {
     const int tok = tid / K, k = tid % K;
     const int e = s_e[tok][k];
+    // rank = earlier tokens' slots holding e (a token's own K experts are
+    // distinct), two tokens' rows per batch as 16-byte reads all in flight
     int rank = 0;
-    for (int t2 = 0; t2 < tok; ++t2)
-      for (int k2 = 0; k2 < K; ++k2) rank += s_e[t2][k2] == e ? 1 : 0;
+    for (int t2 = 0; t2 < tok; t2 += 2) {
+      int4 v[2][kMaxK / 4];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int q = 0; q < kMaxK / 4; ++q)
+          v[a][q] = t2 + a < tok ? *reinterpret_cast<const int4*>(&s_e[t2 + a][4 * q]) : make_int4(-1, -1, -1, -1);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int q = 0; q < kMaxK / 4; ++q)
+          rank += (v[a][q].x == e) + (v[a][q].y == e) + (v[a][q].z == e) + (v[a][q].w == e);
+    }
     const int p = (SCAN ? s_base[e] : base[(int64_t)blockIdx.x * E + e]) + rank;
     if (writer) {
       pos[(int64_t)(t0 + tok) * K + k] = p;
