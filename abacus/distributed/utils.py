@@ -1,10 +1,11 @@
 """abacus.distributed.utils: process-group set-up that the training examples import
 (abacus/distributed/utils.py:9-46).
 
-Same names, arguments and behaviour as the reference's helpers.  This build runs the
-MoE layer on one GPU, so the multi-process paths that use these (data, tensor,
-pipeline and expert parallelism) are not part of it; a single process needs none of
-them, and rank() / world_size() answer 0 and 1 when no process group is initialised.
+Same names, arguments and behaviour as the reference's helpers: rank() and
+world_size() are the process group's (torch.distributed raises when none is
+initialised, as in the reference).  This build runs the MoE layer on one GPU, so the
+multi-process paths that use these (data, tensor, pipeline and expert parallelism)
+are not part of it; a single process needs none of them.
 """
 
 from __future__ import annotations
@@ -37,11 +38,11 @@ def shutdown() -> None:
 
 
 def rank() -> int:
-    return dist.get_rank() if dist.is_initialized() else 0
+    return dist.get_rank()
 
 
 def world_size() -> int:
-    return dist.get_world_size() if dist.is_initialized() else 1
+    return dist.get_world_size()
 
 
 def print_peak_memory() -> None:

@@ -33,7 +33,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_abi_version": (_I, []),
     "abacus_moe_hist_len": (_I64, [_I64, _I64]),
     "abacus_moe_router_ws_bytes": (_I64, [_I64, _I64, _I]),
-    "abacus_moe_router_wgrad_ws_bytes": (_I64, [_I64, _I64, _I64]),
+    "abacus_moe_router_wgrad_ws_bytes": (_I64, [_I64, _I64, _I64, _I]),
     "abacus_moe_down_fwd_ws_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "abacus_moe_load_balancing_ws_bytes": (_I64, [_I64, _I64]),
     "abacus_moe_load_balancing_fwd": (_I, [_P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P, _P]),

@@ -6,7 +6,8 @@
 // kernel when --liger is set.  Here:
 //   forward   one pass over each row: lse_i = log(sum_j exp(x_ij)) in fp32
 //             (running max and rescaled sum, base 2), loss_i = lse_i - x_i[t_i]
-//             (0 for ignored rows)
+//             (0 for ignored rows, NaN for a target outside [0, V) that is
+//             not ignore_index: the loss shows it, and nothing waits on the host)
 //   backward  one pass: dx_ij = g * scale * (exp(x_ij - lse_i) - [j == t_i]),
 //             0 on ignored rows, rounded once to the logits' dtype (bf16 pairs by
 //             one hardware conversion, round to nearest even); g is read
@@ -136,7 +137,8 @@ __global__ __launch_bounds__(256) void ce_fwd_kernel(const T* __restrict__ x, co
     const float l = (m + __builtin_amdgcn_logf(s)) * kLn2;
     lse[row] = l;
     const int64_t t = tgt[row];
-    loss[row] = (t != ignore_index && t >= 0 && t < V) ? l - to_f32<T>(xr[t]) : 0.f;
+    // a target outside [0, V) that is not ignore_index makes the row's loss NaN (no logit read)
+    loss[row] = t == ignore_index ? 0.f : ((t >= 0 && t < V) ? l - to_f32<T>(xr[t]) : __builtin_nanf(""));
   }
 }
 

@@ -420,11 +420,11 @@ void router_wgrad(const T* x, const float* dlogit, const int32_t* idx, int64_t T
 extern "C" {
 
 const char* abacus_moe_last_error(void) { return g_error; }
-int abacus_moe_abi_version(void) { return 3; }
+int abacus_moe_abi_version(void) { return 4; }
 
 int64_t abacus_moe_hist_len(int64_t T, int64_t E) { return ((T + kTokBlock - 1) / kTokBlock) * E; }
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype) { return (int64_t)e_pad(E) * D * elem(dtype); }
-int64_t abacus_moe_router_wgrad_ws_bytes(int64_t, int64_t, int64_t) { return 0; }
+int64_t abacus_moe_router_wgrad_ws_bytes(int64_t, int64_t, int64_t, int) { return 0; }
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t, int64_t, int64_t, int64_t, int) { return 0; }
 
 int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,

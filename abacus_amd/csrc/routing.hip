@@ -18,6 +18,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "device_table.h"
 
 namespace abacus {
 
@@ -1508,35 +1509,60 @@ inline int64_t router_part_bytes(int64_t E) { return (int64_t)kRouterSplit * kRo
 // The allocation-free router weight gradient's partial sums: a static device
 // array, one copy per GPU, held until the process ends.  Host code must never
 // pass `scratch` itself to a kernel (its host-side name is only a handle):
-// scratch_ptr() looks up this GPU's address of it once per device, with that
-// device current, and every launch takes that address.  Calls that overlap on
-// one GPU share the array and race.
+// scratch_ptr() looks up the address of the stream's GPU's copy once per
+// device, with that device current, and every launch takes that address.
+// Calls that overlap on one GPU share the array and race.
 constexpr int64_t kScratchBytes = 32ll << 20;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
-constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-float* g_scratch_dev[kMaxScratchDevices] = {};
+// Device indices 0..1023: far beyond the GPUs one node holds.
+PerDeviceAddress<1024> g_scratch_addr;
 
-// This device's address of `scratch` (nullptr, with the error set, on failure).
-float* scratch_ptr() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
-    set_error("router_wgrad_noalloc: no current HIP device (or device index beyond %d)", kMaxScratchDevices - 1);
+// The address of `scratch` on the device that owns `stream` (the current
+// device for the null stream).  A stream of another device than the current
+// one is rejected (1): the symbol lookup runs on the current device.  nullptr
+// with *rc set (1 rejected, 2 runtime failure) and the error message on failure.
+float* scratch_ptr(hipStream_t stream, int* rc) {
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) {
+    *rc = 2;
+    set_error("router_wgrad_noalloc: no current HIP device");
     return nullptr;
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_dev[dev] == nullptr) {
-    void* p = nullptr;
-    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (rc != hipSuccess || p == nullptr) {
-      set_error("router_wgrad_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
-                hipGetErrorString(rc));
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) {
+      *rc = 2;
+      set_error("router_wgrad_noalloc: hipStreamGetDevice failed for the stream argument");
       return nullptr;
     }
-    g_scratch_dev[dev] = static_cast<float*>(p);
+    dev = (int)sdev;
   }
-  return g_scratch_dev[dev];
+  if (dev != cur) {
+    *rc = 1;
+    set_error("router_wgrad_noalloc: the stream belongs to device %d but device %d is current; make the "
+              "stream's device current before the call", dev, cur);
+    return nullptr;
+  }
+  if (dev > decltype(g_scratch_addr)::kMaxDevice) {
+    *rc = 1;
+    set_error("router_wgrad_noalloc: device index %d beyond %d", dev, decltype(g_scratch_addr)::kMaxDevice);
+    return nullptr;
+  }
+  hipError_t lookup_rc = hipSuccess;
+  void* p = g_scratch_addr.get(dev, [&lookup_rc](int) -> void* {
+    void* a = nullptr;
+    lookup_rc = hipGetSymbolAddress(&a, HIP_SYMBOL(scratch));
+    return lookup_rc == hipSuccess ? a : nullptr;
+  });
+  if (p == nullptr) {
+    *rc = 2;
+    set_error("router_wgrad_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+              hipGetErrorString(lookup_rc));
+    return nullptr;
+  }
+  return static_cast<float*>(p);
 }
 
 // Column chunks of the gather: enough of them for ~1024 blocks, each at least
@@ -1843,42 +1869,45 @@ static bool router_wgrad_mfma_path(int64_t D, int64_t E, int dtype) { return dty
 // partials of at most half the bytes of x, at most kWgradChunkMax (register
 // path) or kWideChunkMax (wide path) tokens.
 // path: 0 register kernel, 1 wide VALU kernel, 2 matrix-core kernel.
-static int router_wgrad_path(int64_t D, int64_t E, int dtype) {
-  return router_wgrad_reg_path(D, E, dtype) ? 0 : (router_wgrad_mfma_path(D, E, dtype) ? 2 : 1);
-}
-static void router_wgrad_plan(int64_t T, int64_t D, int64_t E, int dtype, int path, int* chunk, int* nchunks) {
-  const int64_t cols_per_block = path == 0 ? 64 * wgrad_cpt(dtype) : (path == 2 ? rwg::TD : kWideCols);
+// The plan is made once per call and drives both the workspace size and the
+// launch, so a size check and the launch it guards cannot disagree.
+struct WgradPlan {
+  int path;
+  int chunk;
+  int nchunks;
+  int64_t partial_bytes;  // fp32 partial sums the launch writes: nchunks * E * D * 4
+};
+
+static WgradPlan router_wgrad_plan(int64_t T, int64_t D, int64_t E, int dtype) {
+  WgradPlan p;
+  p.path = router_wgrad_reg_path(D, E, dtype) ? 0 : (router_wgrad_mfma_path(D, E, dtype) ? 2 : 1);
+  const int64_t cols_per_block = p.path == 0 ? 64 * wgrad_cpt(dtype) : (p.path == 2 ? rwg::TD : kWideCols);
   const int64_t dblocks = (D + cols_per_block - 1) / cols_per_block;
-  const int64_t eblocks = path == 2 ? (E + rwg::TE - 1) / rwg::TE : 1;
+  const int64_t eblocks = p.path == 2 ? (E + rwg::TE - 1) / rwg::TE : 1;
   const int64_t elem = dtype == kBF16 ? 2 : 4;
   int64_t nc = std::max<int64_t>(1, 512 / (dblocks * eblocks));
   nc = std::min<int64_t>(nc, std::max<int64_t>(1, T * elem / (8 * E)));
   nc = std::min<int64_t>(nc, std::max<int64_t>(1, T));
   int64_t ch = (T + nc - 1) / nc;
   if (ch < 1) ch = 1;
-  if (path == 0 && ch > kWgradChunkMax) ch = kWgradChunkMax;
-  if (path == 1 && ch > kWideChunkMax) ch = kWideChunkMax;
-  if (path == 2) ch = (ch + rwg::TS - 1) / rwg::TS * rwg::TS;  // whole LDS stages
-  *chunk = (int)ch;
-  *nchunks = (int)std::max<int64_t>(1, (T + ch - 1) / ch);
+  if (p.path == 0 && ch > kWgradChunkMax) ch = kWgradChunkMax;
+  if (p.path == 1 && ch > kWideChunkMax) ch = kWideChunkMax;
+  if (p.path == 2) ch = (ch + rwg::TS - 1) / rwg::TS * rwg::TS;  // whole LDS stages
+  p.chunk = (int)ch;
+  p.nchunks = (int)std::max<int64_t>(1, (T + ch - 1) / ch);
+  p.partial_bytes = (int64_t)p.nchunks * E * D * (int64_t)sizeof(float);
+  return p;
 }
 
-int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E) {
-  // sized for the larger of the two dtypes' plans
-  int64_t best = 0;
-  for (int dtype : {kF32, kBF16}) {
-    int chunk, nchunks;
-    router_wgrad_plan(T, D, E, dtype, router_wgrad_path(D, E, dtype), &chunk, &nchunks);
-    best = std::max<int64_t>(best, (int64_t)nchunks * E * D * 4);
-  }
-  return best;
+int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E, int dtype) {
+  if (dtype != kF32 && dtype != kBF16) return -1;
+  return router_wgrad_plan(T, D, E, dtype).partial_bytes;
 }
 
-static int router_wgrad_launch(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
-                               int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, hipStream_t s) {
-  const int path = router_wgrad_path(D, E, dtype);
-  int chunk, nchunks;
-  router_wgrad_plan(T, D, E, dtype, path, &chunk, &nchunks);
+static int router_wgrad_launch(const WgradPlan& plan, const void* x_TD, const float* dlogit_TK,
+                               const int32_t* idx_TK, int64_t T, int64_t D, int64_t E, int64_t K, int dtype,
+                               float* partial_ws, void* dw_DE, hipStream_t s) {
+  const int path = plan.path, chunk = plan.chunk, nchunks = plan.nchunks;
   // With T == 0 the partial kernel visits no tokens and writes zero partials.
   if (path == 2) {
     const dim3 g1((unsigned)((D + rwg::TD - 1) / rwg::TD), (unsigned)nchunks, (unsigned)((E + rwg::TE - 1) / rwg::TE));
@@ -1935,22 +1964,23 @@ static int check_router_wgrad(int64_t E, int64_t K, int dtype) {
 int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
                             int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream) {
   if (check_router_wgrad(E, K, dtype)) return 1;
-  return router_wgrad_launch(x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype, partial_ws, dw_DE, (hipStream_t)stream);
+  return router_wgrad_launch(router_wgrad_plan(T, D, E, dtype), x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype,
+                             partial_ws, dw_DE, (hipStream_t)stream);
 }
 
 int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T,
                                     int64_t D, int64_t E, int64_t K, int dtype, void* dw_DE, void* stream) {
   if (check_router_wgrad(E, K, dtype)) return 1;
-  int chunk, nchunks;
-  router_wgrad_plan(T, D, E, dtype, router_wgrad_reg_path(D, E, dtype), &chunk, &nchunks);
-  const int64_t need = (int64_t)nchunks * E * D * (int64_t)sizeof(float);
-  ABACUS_CHECK_ARG(need <= kScratchBytes,
+  const WgradPlan plan = router_wgrad_plan(T, D, E, dtype);
+  ABACUS_CHECK_ARG(plan.partial_bytes <= kScratchBytes,
                    "router_wgrad_noalloc: T=%lld D=%lld E=%lld needs %lld bytes of partial sums, more than the "
                    "library's %lld-byte static scratch; call abacus_moe_router_wgrad with a workspace",
-                   (long long)T, (long long)D, (long long)E, (long long)need, (long long)kScratchBytes);
-  float* partial = scratch_ptr();
-  if (partial == nullptr) return 2;
-  return router_wgrad_launch(x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype, partial, dw_DE, (hipStream_t)stream);
+                   (long long)T, (long long)D, (long long)E, (long long)plan.partial_bytes,
+                   (long long)kScratchBytes);
+  int rc = 0;
+  float* partial = scratch_ptr((hipStream_t)stream, &rc);
+  if (partial == nullptr) return rc;
+  return router_wgrad_launch(plan, x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype, partial, dw_DE, (hipStream_t)stream);
 }
 
 int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, float speed, int dtype, void* bias_E,

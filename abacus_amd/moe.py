@@ -98,7 +98,7 @@ def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos
         )
     if ctx_needs_w:
         dw = torch.empty_like(w_DE)
-        nbytes = query("abacus_moe_router_wgrad_ws_bytes", T, D, E, device=dev)
+        nbytes = query("abacus_moe_router_wgrad_ws_bytes", T, D, E, dt, device=dev)
         partial = torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
         call("abacus_moe_router_wgrad", ptr(x_TD), ptr(dlogit), ptr(idx32), T, D, E, K, dt, ptr(partial), ptr(dw), s)
     return dx, dw

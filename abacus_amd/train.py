@@ -80,9 +80,10 @@ def cross_entropy(input: torch.Tensor, target: torch.Tensor, weight: torch.Tenso
 
     (N, V) GPU logits in fp32 or bf16 with the default options (mean over the rows whose
     target is not ignore_index, no class weights or label smoothing) take the HIP kernels.
-    Everything else is torch's cross_entropy.  A target outside [0, V) other than
-    ignore_index raises IndexError before any launch, as torch's CPU kernel does (one host
-    sync reads the row count and the out-of-range count together).
+    Everything else is torch's cross_entropy.  Nothing waits on the host: the row count stays
+    on the device, and a target outside [0, V) other than ignore_index makes the loss NaN (torch's
+    GPU kernel stops on a device assertion there; next_token_loss, which syncs once for its count,
+    raises IndexError instead).
     """
     if _use_liger and input.device.type != "cuda":
         raise RuntimeError("Liger cross entropy needs a CUDA tensor")
@@ -93,13 +94,7 @@ def cross_entropy(input: torch.Tensor, target: torch.Tensor, weight: torch.Tenso
         return F.cross_entropy(input, target, weight=weight, size_average=size_average, ignore_index=ignore_index,
                                reduce=reduce, reduction=reduction, label_smoothing=label_smoothing)
     t = target.to(torch.int64).contiguous()
-    V = input.shape[1]
-    kept = t != ignore_index
-    bad = kept & ((t < 0) | (t >= V))
-    counts = torch.stack([kept.sum(), bad.sum()])
-    if int(counts[1]):  # host sync
-        raise IndexError(f"Target {int(t[bad][0])} is out of bounds.")
-    count = counts[0].to(torch.float32)
+    count = (t != ignore_index).sum().to(torch.float32)
     return _CrossEntropyFunction.apply(input.contiguous(), t, count, int(ignore_index)).to(input.dtype)
 
 

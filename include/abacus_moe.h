@@ -42,8 +42,9 @@ enum { ABACUS_F32 = 0, ABACUS_BF16 = 1 };
 
 /* ---- library / sizing queries ------------------------------------------ */
 const char* abacus_moe_last_error(void);
-/* 3: abacus_moe_router_ws_bytes also covers the small-batch router's partial
- * logits (size the workspace by the query, never by a formula). */
+/* 4: abacus_moe_router_wgrad_ws_bytes takes the dtype (the partial-sum plan
+ * differs by dtype).  3: abacus_moe_router_ws_bytes also covers the small-batch
+ * router's partial logits (size workspaces by the queries, never by a formula). */
 int abacus_moe_abi_version(void);
 /* int32 elements of the per-token-block expert histogram (and of `base`). */
 int64_t abacus_moe_hist_len(int64_t T, int64_t E);
@@ -51,8 +52,9 @@ int64_t abacus_moe_hist_len(int64_t T, int64_t E);
  * transposed router weight and, for bf16 with E <= 64, room for the partial
  * logits of router_fwd's split small-batch pass (T <= 1024); independent of T. */
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
-/* bytes of the fp32 partial-sum scratch used by router_wgrad. */
-int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E);
+/* bytes of the fp32 partial-sum scratch used by router_wgrad for this dtype
+ * (-1 for an unknown dtype). */
+int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E, int dtype);
 /* bytes of the split-tail workspace of down_fwd (0: that shape runs no split, which
  * includes small batches: R <= 128 * E). */
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype);
@@ -185,8 +187,10 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
  * hipMalloc).  The same kernels and the same result bit for bit, with the partial
  * sums in a static 32 MiB device array of the library (one per GPU, held until the
  * process ends) instead of partial_ws.  Shapes whose partial sums need more than
- * 32 MiB are rejected (1) before any launch; abacus_moe_router_wgrad_ws_bytes bounds
- * that need.  Calls that overlap on one GPU share that array and race. */
+ * 32 MiB are rejected (1) before any launch; abacus_moe_router_wgrad_ws_bytes(T, D, E,
+ * dtype) is that need.  The array used is the one of the stream's device, which must be
+ * the current device (a stream of another device is rejected (1); the null stream is the
+ * current device's).  Calls that overlap on one GPU share that array and race. */
 int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T,
                                     int64_t D, int64_t E, int64_t K, int dtype, void* dw_DE, void* stream);
 

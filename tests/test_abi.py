@@ -51,13 +51,13 @@ def test_host_library_exports_its_entry_points():
     assert len(_lib.HOST_SYMBOLS) >= 25
     for name in _lib.HOST_SYMBOLS:
         assert name in decls and hasattr(lib, name), name
-    assert _lib.load_host().abacus_moe_abi_version() == 3
+    assert _lib.load_host().abacus_moe_abi_version() == 4
     assert _lib.query("abacus_moe_hist_len", 4096, 8, device=torch.device("cpu")) == (4096 // 16) * 8
 
 
 def test_abi_version_and_queries():
     lib = _lib.load()
-    assert lib.abacus_moe_abi_version() == 3
+    assert lib.abacus_moe_abi_version() == 4
     assert _lib.query("abacus_moe_hist_len", 4096, 8) == (4096 // 16) * 8
     assert _lib.query("abacus_moe_hist_len", 17, 8) == 2 * 8
     # bf16 with at most 64 experts: the transposed weight, then fp32 partial logits
@@ -65,7 +65,8 @@ def test_abi_version_and_queries():
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 8, _lib.BF16) == 16 * 4096 * 2 + 8 * 1024 * 16 * 4
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 128, _lib.BF16) == 128 * 4096 * 2
     assert _lib.query("abacus_moe_router_ws_bytes", 1024, 17, _lib.F32) == 32 * 1024 * 4
-    assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8) > 0
+    assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8, _lib.BF16) > 0
+    assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8, 7) == -1
     # the down projection's split tail needs a workspace at the Mixtral shape, none for small batches
     assert _lib.query("abacus_moe_down_fwd_ws_bytes", 8192, 14336, 4096, 8, _lib.BF16) > 0
     assert _lib.query("abacus_moe_down_fwd_ws_bytes", 384, 1408, 2048, 64, _lib.BF16) == 0

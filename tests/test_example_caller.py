@@ -96,8 +96,11 @@ def test_example_trains_on_cpu(tmp_path, monkeypatch):
 
 def test_process_group_helpers_single_process(monkeypatch):
     """init_process_group / rank / world_size / shutdown (distributed/utils.py:9-33) as a one-rank
-    gloo group over the loopback interface; rank 0 and world size 1 without a group."""
-    assert (rank(), world_size()) == (0, 1)
+    gloo group over the loopback interface.  Without a group they raise, as torch.distributed's
+    get_rank / get_world_size do in the reference."""
+    for fn in (rank, world_size):
+        with pytest.raises((ValueError, RuntimeError)):
+            fn()
     monkeypatch.setenv("RANK", "0")
     monkeypatch.setenv("WORLD_SIZE", "1")
     monkeypatch.setenv("MASTER_ADDR", "127.0.0.1")
@@ -111,4 +114,5 @@ def test_process_group_helpers_single_process(monkeypatch):
     finally:
         shutdown()
         torch.set_num_threads(threads)
-    assert (rank(), world_size()) == (0, 1)
+    with pytest.raises((ValueError, RuntimeError)):
+        rank()

@@ -1,9 +1,10 @@
 """abacus_moe_router_wgrad_noalloc: the router weight gradient with its partial sums in the
 library's static device scratch instead of a caller workspace.  Through the C ABI, its output
 equals abacus_moe_router_wgrad's bit for bit, on two calls in a row (the second on a smaller
-input, so the scratch still holds the first call's partials), for both dtypes and both partial
-kernels (E <= 16 register path, E > 16 column path); a shape whose partial sums exceed the
-scratch is rejected before any launch."""
+input, so the scratch still holds the first call's partials), on each of the three partial
+kernels: bf16 with D a multiple of 8 (matrix-core kernel), fp32 with E <= 16 (register kernel),
+fp32 with E > 16 (wide column kernel, including shapes whose partial sums fill the 32 MiB scratch
+exactly); a shape whose partial sums exceed the scratch is rejected before any launch."""
 
 import pytest
 import torch
@@ -25,7 +26,8 @@ def _inputs(T, D, E, K, dtype, seed):
 def _with_workspace(x, dlogit, idx, E):
     T, D = x.shape
     K = idx.shape[1]
-    ws = torch.empty(query("abacus_moe_router_wgrad_ws_bytes", T, D, E) // 4 + 1, dtype=torch.float32, device=DEV)
+    nbytes = query("abacus_moe_router_wgrad_ws_bytes", T, D, E, _lib.dtype_code(x.dtype))
+    ws = torch.empty(nbytes // 4 + 1, dtype=torch.float32, device=DEV)
     dw = torch.full((D, E), float("nan"), dtype=x.dtype, device=DEV)
     call("abacus_moe_router_wgrad", ptr(x), ptr(dlogit), ptr(idx), T, D, E, K, _lib.dtype_code(x.dtype), ptr(ws),
          ptr(dw), _lib.stream_of(DEV))
@@ -49,6 +51,22 @@ def test_noalloc_equals_workspace_entry_point(dtype, T, D, E, K, T2):
     print(f"\n[noalloc] T={T} then {T2} D={D} E={E} K={K} {dtype}", flush=True)
     for n, seed in ((T, 1), (T2, 2)):
         x, dlogit, idx = _inputs(n, D, E, K, dtype, seed)
+        got = _noalloc(x, dlogit, idx, E)
+        want = _with_workspace(x, dlogit, idx, E)
+        torch.cuda.synchronize()
+        assert not torch.isnan(want).any()
+        assert torch.equal(got, want), f"T={n}: noalloc differs from the workspace entry point"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,D,E,K,T2", [(8192, 2048, 64, 6, 3000), (8192, 2048, 32, 4, 1500)],
+                         ids=["E64_full_scratch", "E32_full_scratch"])
+def test_noalloc_fp32_wide_path_at_the_scratch_limit(T, D, E, K, T2):
+    """fp32 with E > 16 (the wide column kernel) at shapes whose partial sums are exactly 32 MiB."""
+    assert query("abacus_moe_router_wgrad_ws_bytes", T, D, E, _lib.F32) == 32 << 20
+    print(f"\n[noalloc] fp32 wide T={T} then {T2} D={D} E={E} K={K}", flush=True)
+    for n, seed in ((T, 3), (T2, 4)):
+        x, dlogit, idx = _inputs(n, D, E, K, torch.float32, seed)
         got = _noalloc(x, dlogit, idx, E)
         want = _with_workspace(x, dlogit, idx, E)
         torch.cuda.synchronize()
