@@ -14,6 +14,7 @@ from abacus_amd import _lib
 from abacus_amd import workloads as W
 from abacus.mlp import MLP
 from abacus.moe.moe import MoE, MoEExpertParallel
+from bench_inputs import bench_inputs
 from oracle import moe_oracle as oracle
 
 pytestmark = pytest.mark.gpu
@@ -137,13 +138,22 @@ def test_matches_cpu_oracle(wl, backward):
 
 
 # ---------------- the oracle's torch ops on the GPU, full sizes ----------------
+# On the exact inputs bench.py times (the host recipe), and on a second draw of every workload's
+# distributions made on the GPU.
 FULL_CASES = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K]
 
 
 @pytest.mark.parametrize("wl", FULL_CASES, ids=[w.name for w in FULL_CASES])
 def test_matches_reference_full_size(wl):
     print(f"\n[moe-full] {wl.name} T={wl.tokens} D={wl.dim} E={wl.n_experts} K={wl.top_k} M={wl.hidden} "
-          f"bwd={wl.backward}", flush=True)
+          f"bwd={wl.backward} (bench inputs)", flush=True)
+    moe, x, target = bench_inputs(wl, DEV)
+    check_against(moe, x, target, DEV, wl.backward)
+
+
+@pytest.mark.parametrize("wl", FULL_CASES, ids=[w.name for w in FULL_CASES])
+def test_matches_reference_full_size_device_draw(wl):
+    print(f"\n[moe-full] {wl.name} (values drawn on the GPU)", flush=True)
     moe, x, target = W.build_on_device(wl, DEV)
     check_against(moe, x, target, DEV, wl.backward)
 

@@ -10,6 +10,7 @@ import torch
 
 from abacus_amd import workloads as W
 from abacus.moe.router import Router
+from bench_inputs import bench_inputs
 from oracle import moe_oracle as oracle
 from routing_check import check_against_torch_topk
 from special_selection import SPECIAL_CASES, check_special_selection
@@ -17,27 +18,23 @@ from special_selection import SPECIAL_CASES, check_special_selection
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 
-# (workload, build on CPU with the exact recipe?)  Large weights are drawn on the GPU.
-CASES = [
-    (W.TINY_F32, True),
-    (W.MID_F32, True),
-    (W.MIXTRAL_BF16, False),
-    (W.SKEW_BF16_T64, False),
-    (W.SKEW_BF16_T512, False),
-    (W.SKEW_BF16_T16K, False),
-]
+# (workload, the exact inputs bench.py times?)  Otherwise a second draw of the same
+# distributions, made on the GPU.
+WORKLOADS = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K]
+CASES = [(w, True) for w in WORKLOADS] + [(w, False) for w in WORKLOADS if w.dim * w.n_experts >= 2**16]
 
 
-def build(wl, on_cpu):
-    if on_cpu:
-        return W.build(wl, device=DEV)
+def build(wl, bench):
+    if bench:
+        return bench_inputs(wl, DEV)
     return W.build_on_device(wl, DEV)
 
 
-@pytest.mark.parametrize("wl,on_cpu", CASES, ids=[c[0].name for c in CASES])
-def test_routing_bit_exact(wl, on_cpu):
-    print(f"\n[routing] {wl.name} T={wl.tokens} D={wl.dim} E={wl.n_experts} K={wl.top_k}", flush=True)
-    moe, x, _ = build(wl, on_cpu)
+@pytest.mark.parametrize("wl,bench", CASES, ids=[c[0].name + ("" if c[1] else "-device_draw") for c in CASES])
+def test_routing_bit_exact(wl, bench):
+    print(f"\n[routing] {wl.name} T={wl.tokens} D={wl.dim} E={wl.n_experts} K={wl.top_k} "
+          f"{'bench inputs' if bench else 'drawn on the GPU'}", flush=True)
+    moe, x, _ = build(wl, bench)
     moe.train()
     bias0 = moe.router.expert_bias_E.detach().clone()
     with torch.no_grad():
