@@ -132,6 +132,26 @@ template <> struct VecTraits<uint16_t> {
 
 __device__ inline Vec16 ld16(const void* p) { return *reinterpret_cast<const Vec16*>(p); }
 __device__ inline void st16(void* p, const Vec16& v) { *reinterpret_cast<Vec16*>(p) = v; }
+// Nontemporal 16-byte loads and stores, for data a pass touches once: they keep
+// it out of the caches' working set.
+typedef unsigned int u32x4_nt_t __attribute__((ext_vector_type(4)));
+__device__ inline Vec16 ld16_stream(const void* p) {
+  const u32x4_nt_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt_t*>(p));
+  Vec16 r;
+  r.w[0] = v.x;
+  r.w[1] = v.y;
+  r.w[2] = v.z;
+  r.w[3] = v.w;
+  return r;
+}
+__device__ inline void st16_stream(void* p, const Vec16& x) {
+  u32x4_nt_t v;
+  v.x = x.w[0];
+  v.y = x.w[1];
+  v.z = x.w[2];
+  v.w = x.w[3];
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4_nt_t*>(p));
+}
 __device__ inline Vec16 zero16() {
   Vec16 v;
   v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;

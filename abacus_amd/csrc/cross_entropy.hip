@@ -30,26 +30,8 @@ constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Logits are read once per pass: nontemporal loads and stores keep them out
-// of the caches' working set.
-typedef unsigned int ce_u32x4 __attribute__((ext_vector_type(4)));
-__device__ inline Vec16 ld16_stream(const void* p) {
-  const ce_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const ce_u32x4*>(p));
-  Vec16 r;
-  r.w[0] = v.x;
-  r.w[1] = v.y;
-  r.w[2] = v.z;
-  r.w[3] = v.w;
-  return r;
-}
-__device__ inline void st16_stream(void* p, const Vec16& x) {
-  ce_u32x4 v;
-  v.x = x.w[0];
-  v.y = x.w[1];
-  v.z = x.w[2];
-  v.w = x.w[3];
-  __builtin_nontemporal_store(v, reinterpret_cast<ce_u32x4*>(p));
-}
+// Logits are read once per pass: nontemporal loads and stores (ld16_stream,
+// st16_stream) keep them out of the caches' working set.
 
 // g * exp2(x * log2e - l2) for the 8 bf16 / 4 fp32 elements of a vector,
 // stored in the logits' dtype (bf16 pairs by one hardware conversion).

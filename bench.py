@@ -76,6 +76,13 @@ def hbm_bytes(wl, name):
         return s * D * (T + 2 * R) + (s + 4 + 4 + 4) * R
     if name == "abacus_moe_unpermute_bwd":
         return s * D * (R + T) + (4 + 4 + 4) * R
+    E = wl.n_experts
+    if name == "abacus_moe_router_fwd":
+        # read x and w_DE; write logits, weights, int64 + int32 indices and fp32 scores
+        return s * T * D + s * D * E + s * T * E + (s + 8 + 4 + 4) * T * K
+    if name == "abacus_moe_router_wgrad":
+        # read x, the fp32 dlogits and int32 indices; write dW_DE
+        return s * T * D + (4 + 4) * T * K + s * D * E
     return None
 
 
