@@ -58,6 +58,10 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU-baseline sample duration")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="skip the HIP-graph replay of forward-only workloads")
+    p.add_argument("--vendor-gemm", action="store_true",
+                   help="instead of the layer step: time hipBLASLt (torch.mm) on the same per-expert products "
+                        "as the four grouped-GEMM entry points, with the workload's own routing (a reference "
+                        "point for the GEMM kernels; no fused epilogues)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="after the timed steps, copy 1 GiB device-to-device once (a known-size kernel "
                         "to scale FETCH_SIZE / WRITE_SIZE counters against)")
@@ -250,6 +254,76 @@ def bench_decoder(args, dtype):
     }
 
 
+def bench_vendor_gemm(args, wl, moe, x):
+    """hipBLASLt (torch.mm on 2-D operands) on the per-expert products of the four grouped-GEMM
+    entry points, expert by expert with the workload's routing: the vendor library's rate on the
+    same shapes (operands N(0,1) activations and the module's weights; the library's own kernels
+    see no SwiGLU, scaling or fused outputs, so this is a lower bound on their work)."""
+    dev = x.device
+    moe.eval()
+    with torch.no_grad():
+        moe(x)
+    counts = [int(c) for c in moe.router.last_routing.counts_E.tolist()]
+    D, M, dt = wl.dim, wl.hidden, wl.dtype
+    g = torch.Generator(device=dev).manual_seed(wl.seed)
+
+    def act(rows, cols):
+        return torch.randn(rows, cols, device=dev, generator=g).to(dt)
+
+    xs = [act(s, D) for s in counts]
+    hs = [act(s, M) for s in counts]
+    dys = [act(s, D) for s in counts]
+    dgs = [act(s, M) for s in counts]
+    dus = [act(s, M) for s in counts]
+    wg, wu, wd = moe.w_gate_EDM.detach(), moe.w_up_EDM.detach(), moe.w_down_EMD.detach()
+    out_rm = [torch.empty(s, M, device=dev, dtype=dt) for s in counts]
+    out_rd = [torch.empty(s, D, device=dev, dtype=dt) for s in counts]
+    out_dm = torch.empty(D, M, device=dev, dtype=dt)
+    out_md = torch.empty(M, D, device=dev, dtype=dt)
+    experts = [e for e, s in enumerate(counts) if s > 0]
+
+    def gateup_fwd():
+        for e in experts:
+            torch.mm(xs[e], wg[e], out=out_rm[e])
+            torch.mm(xs[e], wu[e], out=out_rm[e])
+
+    def down_fwd():
+        for e in experts:
+            torch.mm(hs[e], wd[e], out=out_rd[e])
+
+    def down_bwd():
+        for e in experts:
+            torch.mm(dys[e], wd[e].t(), out=out_rm[e])   # data gradient (before the SwiGLU backward)
+            torch.mm(hs[e].t(), dys[e], out=out_md)      # weight gradient
+
+    def gateup_bwd():
+        for e in experts:
+            torch.mm(dgs[e], wg[e].t(), out=out_rd[e])   # data gradient, gate half
+            out_rd[e].addmm_(dus[e], wu[e].t())          # + up half
+            torch.mm(xs[e].t(), dgs[e], out=out_dm)      # weight gradients
+            torch.mm(xs[e].t(), dus[e], out=out_dm)
+
+    kinds = {"abacus_moe_gateup_fwd": gateup_fwd, "abacus_moe_down_fwd": down_fwd,
+             "abacus_moe_down_bwd": down_bwd, "abacus_moe_gateup_bwd": gateup_bwd}
+    R = sum(counts)
+    res = {}
+    for name, fn in kinds.items():
+        for _ in range(max(1, args.warmup)):
+            fn()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        ev[0].record()
+        for _ in range(args.steps):
+            fn()
+        ev[1].record()
+        torch.cuda.synchronize()
+        us = ev[0].elapsed_time(ev[1]) * 1000.0 / args.steps
+        tf = GEMM_FLOPS[name] * R * D * M / (us / 1e6) / 1e12
+        res[name] = {"avg_us": round(us, 2), "tflops": round(tf, 1), "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+    return {"vendor_gemm": "hipBLASLt via torch.mm, per expert, the workload's routing",
+            "workload": wl.name, "rows_per_expert": counts, "steps": args.steps, "kinds": res}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -275,6 +349,9 @@ def main():
     # Training workloads run in train mode (the router's bias step included) with the bias reset
     # before every step, so every step routes as the first; forward-only workloads are inference
     # and run in eval mode, where the bias does not move (router.py:53).
+    if args.vendor_gemm:
+        print(json.dumps(bench_vendor_gemm(args, wl, moe, x)), flush=True)
+        return
     moe.train(wl.backward)
     bias0 = moe.router.expert_bias_E.detach().clone()
 
