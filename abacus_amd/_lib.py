@@ -19,6 +19,8 @@ HOST_LIB_PATH = pathlib.Path(__file__).resolve().parent / "lib" / "libabacus_moe
 
 F32 = 0
 BF16 = 1
+F64 = 2  # the host library (CPU tensors) only
+F16 = 3  # the host library (CPU tensors) only
 TILE_CTR_INTS = 16  # ABACUS_MOE_TILE_CTR_INTS
 
 _P = ctypes.c_void_p
@@ -36,19 +38,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_router_wgrad_ws_bytes": (_I64, [_I64, _I64, _I64, _I]),
     "abacus_moe_down_fwd_ws_bytes": (_I64, [_I64, _I64, _I64, _I64, _I]),
     "abacus_moe_load_balancing_ws_bytes": (_I64, [_I64, _I64]),
-    "abacus_moe_load_balancing_fwd": (_I, [_P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P, _P]),
-    "abacus_moe_load_balancing_bwd": (_I, [_P, _P, _I64, _I64, _F, _I, _P, _P]),
+    "abacus_moe_load_balancing_fwd": (_I, [_P, _P, _I64, _I64, _I64, _D, _I, _P, _P, _P, _P, _P, _P]),
+    "abacus_moe_load_balancing_bwd": (_I, [_P, _P, _I64, _I64, _D, _I, _P, _P]),
     "abacus_moe_router_fwd": (
         _I,
-        [_P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _P, _P, _P, _P, _P, _P],
+        [_P, _P, _P, _I64, _I64, _I64, _I64, _D, _I, _P, _P, _P, _P, _P, _P, _P, _P],
     ),
-    "abacus_moe_route_scan": (_I, [_P, _I64, _I64, _I64, _P, _F, _I, _P, _P, _P, _P]),
+    "abacus_moe_route_scan": (_I, [_P, _I64, _I64, _I64, _P, _D, _I, _P, _P, _P, _P]),
     "abacus_moe_permute_gather": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
-    "abacus_moe_dispatch": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _F, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "abacus_moe_dispatch": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _P, _D, _I, _P, _P, _P, _P, _P, _P, _P]),
     "abacus_moe_gateup_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P]),
     "abacus_moe_down_fwd": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _I64, _P]),
     "abacus_moe_combine_fwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I64, _I, _P, _P]),
-    "abacus_moe_combine_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _I, _P, _P, _P]),
+    "abacus_moe_combine_bwd": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _D, _I, _P, _P, _P]),
     "abacus_moe_down_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
     "abacus_moe_down_bwd_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
     "abacus_moe_gateup_bwd_dgrad": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
@@ -58,8 +60,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "abacus_moe_unpermute_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
     "abacus_moe_router_wgrad": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P, _P]),
     "abacus_moe_router_wgrad_noalloc": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _P]),
-    "abacus_router_gating_bwd": (_I, [_P, _P, _P, _I64, _I64, _F, _I, _P, _P]),
-    "abacus_router_update_bias": (_I, [_P, _I64, _I64, _F, _I, _P, _P]),
+    "abacus_router_gating_bwd": (_I, [_P, _P, _P, _I64, _I64, _D, _I, _P, _P]),
+    "abacus_router_update_bias": (_I, [_P, _I64, _I64, _D, _I, _P, _P]),
     "abacus_rmsnorm_fwd": (_I, [_P, _P, _I64, _I64, _F, _I, _P, _P, _P]),
     "abacus_rmsnorm_bwd_ws_bytes": (_I64, [_I64, _I64]),
     "abacus_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _I64, _I64, _I, _P, _P, _P, _I64, _P]),
@@ -207,12 +209,25 @@ def query(name: str, *args, device: torch.device | None = None) -> int:
     return int(getattr(lib, name)(*args))
 
 
-def dtype_code(dtype: torch.dtype) -> int:
+def dtype_code(dtype: torch.dtype, device: torch.device | None = None) -> int:
+    """The ABI dtype code.  float32 and bfloat16 run everywhere; float64 and float16 on CPU
+    tensors only (the host library), and `device` other than the CPU refuses them."""
     if dtype == torch.float32:
         return F32
     if dtype == torch.bfloat16:
         return BF16
-    raise TypeError(f"abacus_amd MoE kernels support float32 and bfloat16, got {dtype}")
+    if dtype in (torch.float64, torch.float16):
+        if device is not None and device.type != "cpu":
+            raise TypeError(f"abacus_amd's HIP kernels take float32 and bfloat16, got {dtype}; float64 and float16 "
+                            "run on CPU tensors (the host library)")
+        return F64 if dtype == torch.float64 else F16
+    raise TypeError(f"abacus_amd MoE kernels support float32, bfloat16, and on CPU tensors float64 and float16; "
+                    f"got {dtype}")
+
+
+def acc_dtype(dtype: torch.dtype) -> torch.dtype:
+    """The dtype of the fp32 side buffers (scores, dlogits, f_E): float64 for float64, else float32."""
+    return torch.float64 if dtype == torch.float64 else torch.float32
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

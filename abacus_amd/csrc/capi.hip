@@ -21,6 +21,6 @@ extern "C" {
 
 const char* abacus_moe_last_error(void) { return abacus::g_error; }
 
-int abacus_moe_abi_version(void) { return 4; }
+int abacus_moe_abi_version(void) { return 5; }
 
 }  // extern "C"

@@ -152,8 +152,10 @@ int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E) {
 }
 
 int abacus_moe_load_balancing_fwd(const void* probs_TE, const int64_t* slots_TK, int64_t T, int64_t E, int64_t K,
-                                  float coeff_e, int dtype, void* ws, float* f_E, float* loss_f32, void* loss_out,
+                                  double coeff_e_d, int dtype, void* ws, float* f_E, float* loss_f32, void* loss_out,
                                   int32_t* bad_index, void* stream) {
+  const float coeff_e = (float)coeff_e_d;
+
   if (check_lb(T, E, K, dtype)) return 1;
   ABACUS_CHECK_ARG(T > 0, "no tokens: the loss is zero and needs no launch");
   const int64_t nb = lb_blocks(T);
@@ -179,8 +181,9 @@ int abacus_moe_load_balancing_fwd(const void* probs_TE, const int64_t* slots_TK,
   return 0;
 }
 
-int abacus_moe_load_balancing_bwd(const void* grad_loss, const float* f_E, int64_t T, int64_t E, float coeff_e,
+int abacus_moe_load_balancing_bwd(const void* grad_loss, const float* f_E, int64_t T, int64_t E, double coeff_e_d,
                                   int dtype, void* grad_probs_TE, void* stream) {
+  const float coeff_e = (float)coeff_e_d;
   if (check_lb(T, E, 1, dtype)) return 1;
   const int64_t n = T * E;
   if (n == 0) return 0;

@@ -1614,9 +1614,11 @@ int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype) {
 }
 
 int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
-                          int64_t K, float route_scale, int dtype, void* logits_TE, void* weights_TK,
-                          int64_t* indices_TK, int32_t* idx_TK, float* score_TK, int32_t* hist, void* wt_ws,
+                          int64_t K, double route_scale_d, int dtype, void* logits_TE, void* weights_TK,
+                          int64_t* indices_TK, int32_t* idx_TK, void* score_ws, int32_t* hist, void* wt_ws,
                           void* stream) {
+  const float route_scale = (float)route_scale_d;
+  float* score_TK = (float*)score_ws;
   if (check_route_shape(T, D, E, K, dtype, false)) return 1;
   hipStream_t s = (hipStream_t)stream;
   const int EP = e_pad(E);
@@ -1688,8 +1690,9 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
 }
 
 int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, void* bias_E,
-                          float bias_update_speed, int dtype, int32_t* base, int32_t* counts_E,
+                          double bias_update_speed_d, int dtype, int32_t* base, int32_t* counts_E,
                           int32_t* offsets_E1, void* stream) {
+  const float bias_update_speed = (float)bias_update_speed_d;
   if (check_dtype(dtype)) return 1;
   ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
   ABACUS_CHECK_ARG(T >= 0 && T * K < (1ll << 31), "bad token count %lld", (long long)T);
@@ -1733,9 +1736,10 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
 }
 
 int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* idx_TK, int64_t T, int64_t D,
-                        int64_t E, int64_t K, void* bias_E, float bias_update_speed, int dtype, int32_t* counts_E,
+                        int64_t E, int64_t K, void* bias_E, double bias_update_speed_d, int dtype, int32_t* counts_E,
                         int32_t* offsets_E1, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD, int32_t* base_ws,
                         void* stream) {
+  const float bias_update_speed = (float)bias_update_speed_d;
   if (check_route_shape(T, D, E, K, dtype)) return 1;
   const int64_t nb = (T + kRouteTB - 1) / kRouteTB;
   if (nb * E > kFusedScanInts) {  // the scan as its own launch, then the gather
@@ -1790,9 +1794,12 @@ int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32
   return 0;
 }
 
-int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* weights_TK, const float* score_TK,
-                           const int32_t* pos_TK, int64_t T, int64_t D, int64_t K, float route_scale, int dtype,
-                           void* dy_RD, float* dlogit_TK, void* stream) {
+int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* weights_TK, const void* score_ws,
+                           const int32_t* pos_TK, int64_t T, int64_t D, int64_t K, double route_scale_d, int dtype,
+                           void* dy_RD, void* dlogit_ws, void* stream) {
+  const float* score_TK = (const float*)score_ws;
+  float* dlogit_TK = (float*)dlogit_ws;
+  const float route_scale = (float)route_scale_d;
   if (check_route_shape(T, D, K, K, dtype)) return 1;
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
@@ -1813,8 +1820,11 @@ int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* we
   return 0;
 }
 
-int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const float* score_TK, int64_t T,
-                             int64_t K, float route_scale, int dtype, float* dlogit_TK, void* stream) {
+int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const void* score_ws, int64_t T,
+                             int64_t K, double route_scale_d, int dtype, void* dlogit_ws, void* stream) {
+  const float* score_TK = (const float*)score_ws;
+  float* dlogit_TK = (float*)dlogit_ws;
+  const float route_scale = (float)route_scale_d;
   if (check_dtype(dtype)) return 1;
   ABACUS_CHECK_ARG(K >= 1 && K <= kMaxK, "top_k %lld: supported range 1..%d", (long long)K, kMaxK);
   if (T == 0) return 0;
@@ -1831,9 +1841,10 @@ int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, co
   return 0;
 }
 
-int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, const int32_t* idx_TK,
+int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const void* dlogit_ws, const int32_t* idx_TK,
                              const int32_t* pos_TK, const void* w_DE, void* wt_ws, int64_t T, int64_t D, int64_t E,
                              int64_t K, int dtype, void* dx_TD, void* stream) {
+  const float* dlogit_TK = (const float*)dlogit_ws;
   if (check_route_shape(T, D, E, K, dtype, false)) return 1;
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
@@ -1980,15 +1991,17 @@ static int check_router_wgrad(int64_t E, int64_t K, int dtype) {
   return 0;
 }
 
-int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
+int abacus_moe_router_wgrad(const void* x_TD, const void* dlogit_ws, const int32_t* idx_TK, int64_t T, int64_t D,
                             int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream) {
+  const float* dlogit_TK = (const float*)dlogit_ws;
   if (check_router_wgrad(E, K, dtype)) return 1;
   return router_wgrad_launch(router_wgrad_plan(T, D, E, dtype), x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype,
                              partial_ws, dw_DE, (hipStream_t)stream);
 }
 
-int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T,
+int abacus_moe_router_wgrad_noalloc(const void* x_TD, const void* dlogit_ws, const int32_t* idx_TK, int64_t T,
                                     int64_t D, int64_t E, int64_t K, int dtype, void* dw_DE, void* stream) {
+  const float* dlogit_TK = (const float*)dlogit_ws;
   if (check_router_wgrad(E, K, dtype)) return 1;
   const WgradPlan plan = router_wgrad_plan(T, D, E, dtype);
   ABACUS_CHECK_ARG(plan.partial_bytes <= kScratchBytes,
@@ -2002,8 +2015,9 @@ int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, co
   return router_wgrad_launch(plan, x_TD, dlogit_TK, idx_TK, T, D, E, K, dtype, partial, dw_DE, (hipStream_t)stream);
 }
 
-int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, float speed, int dtype, void* bias_E,
+int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, double speed_d, int dtype, void* bias_E,
                               void* stream) {
+  const float speed = (float)speed_d;
   if (check_dtype(dtype)) return 1;
   ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
   hipStream_t s = (hipStream_t)stream;

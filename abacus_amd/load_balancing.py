@@ -22,7 +22,7 @@ class _LoadBalancingLoss(torch.autograd.Function):
     def forward(ctx, probs_TE: torch.Tensor, slots_TK: torch.Tensor, coeff_e: float):
         T, E = probs_TE.shape
         K = slots_TK.shape[1]
-        dev, dt = probs_TE.device, _lib.dtype_code(probs_TE.dtype)
+        dev, dt = probs_TE.device, _lib.dtype_code(probs_TE.dtype, probs_TE.device)
         ws = torch.empty(_lib.query("abacus_moe_load_balancing_ws_bytes", T, E, device=dev), dtype=torch.uint8,
                          device=dev)
         f_E = torch.empty(E, dtype=torch.float32, device=dev)

@@ -66,12 +66,12 @@ def _router_fwd(x_TD, w_DE, bias_E, top_k, route_scale):
     transposed router weights the kernel made (the backward's un-permute reuses them)."""
     T, D = x_TD.shape
     E = w_DE.shape[1]
-    dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+    dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype, x_TD.device)
     logits = torch.empty(T, E, dtype=x_TD.dtype, device=dev)
     weights = torch.empty(T, top_k, dtype=x_TD.dtype, device=dev)
     indices = torch.empty(T, top_k, dtype=torch.int64, device=dev)
     idx32 = torch.empty(T, top_k, dtype=torch.int32, device=dev)
-    score = torch.empty(T, top_k, dtype=torch.float32, device=dev)
+    score = torch.empty(T, top_k, dtype=_lib.acc_dtype(x_TD.dtype), device=dev)
     hist = torch.empty(query("abacus_moe_hist_len", T, E, device=dev), dtype=torch.int32, device=dev)
     wt = torch.empty(query("abacus_moe_router_ws_bytes", D, E, dt, device=dev), dtype=torch.uint8, device=dev)
     call(
@@ -87,7 +87,7 @@ def _router_dgrad_wgrad(ctx_needs_x, ctx_needs_w, x_TD, w_DE, dlogit, idx32, pos
     T, D = x_TD.shape
     E = w_DE.shape[1]
     K = idx32.shape[1]
-    dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+    dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype, x_TD.device)
     s = _lib.stream_of(dev)
     dx = dw = None
     if ctx_needs_x:
@@ -121,8 +121,8 @@ class _RouterFunction(torch.autograd.Function):
     def backward(ctx, dweights, _dindices):
         x_TD, w_DE, weights, score, idx32, wt = ctx.saved_tensors
         T, K = weights.shape
-        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
-        dlogit = torch.empty(T, K, dtype=torch.float32, device=dev)
+        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype, x_TD.device)
+        dlogit = torch.empty(T, K, dtype=_lib.acc_dtype(x_TD.dtype), device=dev)
         dweights = _contig(dweights.to(weights.dtype))
         call(
             "abacus_router_gating_bwd", ptr(dweights), ptr(weights), ptr(score), T, K, ctx.route_scale, dt,
@@ -143,7 +143,7 @@ class _MoEFunction(torch.autograd.Function):
         E, _, M = w_gate.shape
         K = top_k
         R = T * K
-        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype, x_TD.device)
         s = _lib.stream_of(dev)
         logits, weights, indices, idx32, score, hist, wt = _router_fwd(x_TD, w_DE, bias_E, K, route_scale)
         base = torch.empty_like(hist)
@@ -187,12 +187,12 @@ class _MoEFunction(torch.autograd.Function):
         E, _, M = w_gate.shape
         K = idx32.shape[1]
         R = T * K
-        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype)
+        dev, dt = x_TD.device, _lib.dtype_code(x_TD.dtype, x_TD.device)
         s = _lib.stream_of(dev)
         needs = ctx.needs_input_grad
         dout = _contig(dout.to(x_TD.dtype))
         dy = torch.empty(R, D, dtype=x_TD.dtype, device=dev)
-        dlogit = torch.empty(T, K, dtype=torch.float32, device=dev)
+        dlogit = torch.empty(T, K, dtype=_lib.acc_dtype(x_TD.dtype), device=dev)
         call(
             "abacus_moe_combine_bwd", ptr(dout), ptr(y), ptr(weights), ptr(score), ptr(pos), T, D, K,
             ctx.route_scale, dt, ptr(dy), ptr(dlogit), s,
@@ -245,7 +245,7 @@ def _check_operands(x_BLD: torch.Tensor, *params: torch.Tensor) -> None:
             raise RuntimeError(f"MoE parameter on {p.device} but input on {x_BLD.device}")
         if p.dtype != x_BLD.dtype:
             raise RuntimeError(f"MoE parameter dtype {p.dtype} does not match input dtype {x_BLD.dtype}")
-    _lib.dtype_code(x_BLD.dtype)
+    _lib.dtype_code(x_BLD.dtype, x_BLD.device)
 
 
 class Router(torch.nn.Module):
@@ -307,7 +307,7 @@ class Router(torch.nn.Module):
         idx = _contig(indices_BLK.reshape(-1).to(device=bias.device, dtype=torch.int64))
         call(
             "abacus_router_update_bias", ptr(idx), idx.numel(), self.n_experts, float(self.bias_update_speed),
-            _lib.dtype_code(bias.dtype), ptr(bias), _lib.stream_of(bias.device),
+            _lib.dtype_code(bias.dtype, bias.device), ptr(bias), _lib.stream_of(bias.device),
         )
 
 

@@ -11,9 +11,9 @@
  *   - All pointers are device pointers (HIP, same device), row-major,
  *     contiguous and 16-byte aligned.  Nothing here allocates, frees or
  *     synchronises; every launch goes to `stream` (a hipStream_t).
- *   - dtype: ABACUS_F32 (0) or ABACUS_BF16 (1) for activations and weights;
- *     index tensors are int32 unless named *_i64; score / dlogit buffers are
- *     fp32.
+ *   - dtype: ABACUS_F32 (0) or ABACUS_BF16 (1) for activations and weights
+ *     (the host build also ABACUS_F64 and ABACUS_F16); index tensors are int32
+ *     unless named *_i64; score / dlogit buffers are fp32 (fp64 with fp64).
  *   - Return 0 on success, nonzero on a rejected argument (1) or launch
  *     failure (2); abacus_moe_last_error() gives the message (per thread).
  *   - Sizes: T tokens, D model dim, E experts (<= 256), K slots per token
@@ -32,7 +32,14 @@
 extern "C" {
 #endif
 
-enum { ABACUS_F32 = 0, ABACUS_BF16 = 1 };
+/* ABACUS_F64 and ABACUS_F16 are taken by the host build only (CPU tensors; the
+ * HIP library rejects them).  The acc side buffers (score and
+ * dlogit) hold fp32 elements, fp64 ones for ABACUS_F64; scalar factors
+ * (route_scale, bias speeds) are cast to that type, as torch casts a Python
+ * scalar meeting a tensor of the dtype.  The load-balancing loss computes in
+ * fp32 for every dtype (load_balancing.py:30 casts the probabilities to
+ * float), so its f_E and fp32 loss stay fp32. */
+enum { ABACUS_F32 = 0, ABACUS_BF16 = 1, ABACUS_F64 = 2, ABACUS_F16 = 3 };
 
 /* int32 elements of the tile-counter workspace (tile_ctr) that the weight-gradient
  * entry points take: device memory the call clears on its stream and then uses
@@ -42,9 +49,11 @@ enum { ABACUS_F32 = 0, ABACUS_BF16 = 1 };
 
 /* ---- library / sizing queries ------------------------------------------ */
 const char* abacus_moe_last_error(void);
-/* 4: abacus_moe_router_wgrad_ws_bytes takes the dtype (the partial-sum plan
- * differs by dtype).  3: abacus_moe_router_ws_bytes also covers the small-batch
- * router's partial logits (size workspaces by the queries, never by a formula). */
+/* 5: scalar factors are double and the acc side buffers void* (ABACUS_F64 and
+ * ABACUS_F16 in the host build).  4: abacus_moe_router_wgrad_ws_bytes takes the
+ * dtype (the partial-sum plan differs by dtype).  3: abacus_moe_router_ws_bytes
+ * also covers the small-batch router's partial logits (size workspaces by the
+ * queries, never by a formula). */
 int abacus_moe_abi_version(void);
 /* int32 elements of the per-token-block expert histogram (and of `base`). */
 int64_t abacus_moe_hist_len(int64_t T, int64_t E);
@@ -70,15 +79,15 @@ int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E);
  * idx_TK (int32 copy), score_TK (fp32 value of the dtype-rounded selected
  * sigmoid scores), hist (abacus_moe_hist_len ints). */
 int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
-                          int64_t K, float route_scale, int dtype, void* logits_TE, void* weights_TK,
-                          int64_t* indices_TK_i64, int32_t* idx_TK, float* score_TK, int32_t* hist, void* wt_ws,
+                          int64_t K, double route_scale, int dtype, void* logits_TE, void* weights_TK,
+                          int64_t* indices_TK_i64, int32_t* idx_TK, void* score_TK, int32_t* hist, void* wt_ws,
                           void* stream);
 
 /* Replaces the per-expert counting of moe.py:73-76 and, when bias_E is not
  * NULL, Router.update_bias (router.py:57-70) in place.  Produces counts_E,
  * offsets_E1 and base (per token-block first row of each expert). */
 int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, void* bias_E,
-                          float bias_update_speed, int dtype, int32_t* base, int32_t* counts_E,
+                          double bias_update_speed, int dtype, int32_t* base, int32_t* counts_E,
                           int32_t* offsets_E1, void* stream);
 
 /* Replaces the boolean-mask gather x_TD[selected_T] of moe.py:77 for all
@@ -95,7 +104,7 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
  * scan them themselves and there is one launch; base_ws (hist-length ints)
  * is then unused. */
 int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* idx_TK, int64_t T, int64_t D,
-                        int64_t E, int64_t K, void* bias_E, float bias_update_speed, int dtype, int32_t* counts_E,
+                        int64_t E, int64_t K, void* bias_E, double bias_update_speed, int dtype, int32_t* counts_E,
                         int32_t* offsets_E1, int32_t* pos_TK, int32_t* perm_R, void* x_perm_RD, int32_t* base_ws,
                         void* stream);
 
@@ -126,9 +135,9 @@ int abacus_moe_combine_fwd(const void* y_RD, const void* weights_TK, const int32
 /* Backward of moe.py:81-85 and router.py:45,49-51: dy_RD[pos] =
  * w * dout[t]; dL/dweights = <dout[t], y>; then renormalise and sigmoid
  * backward to dlogit_TK (fp32, one value per selected expert). */
-int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* weights_TK, const float* score_TK,
-                           const int32_t* pos_TK, int64_t T, int64_t D, int64_t K, float route_scale, int dtype,
-                           void* dy_RD, float* dlogit_TK, void* stream);
+int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* weights_TK, const void* score_TK,
+                           const int32_t* pos_TK, int64_t T, int64_t D, int64_t K, double route_scale, int dtype,
+                           void* dy_RD, void* dlogit_TK, void* stream);
 
 /* Backward of moe.py:80 (dgrad) fused with the SwiGLU backward of moe.py:78-79:
  * dh = dy @ w_down[e]^T; dgate = dh*up*silu'(gate); dup = dh*silu(gate). */
@@ -174,12 +183,12 @@ int abacus_moe_gateup_bwd(const void* dgate_RM, const void* dup_RM, const void* 
  * dx_perm_RD may be NULL (router used on its own).  wt_ws receives the
  * transposed router weights; with w_DE NULL it must already hold them, as
  * abacus_moe_router_fwd left them for the same weights. */
-int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const float* dlogit_TK, const int32_t* idx_TK,
+int abacus_moe_unpermute_bwd(const void* dx_perm_RD, const void* dlogit_TK, const int32_t* idx_TK,
                              const int32_t* pos_TK, const void* w_DE, void* wt_ws, int64_t T, int64_t D, int64_t E,
                              int64_t K, int dtype, void* dx_TD, void* stream);
 
 /* Backward of the router GEMM of router.py:45 (wgrad): dw_DE = x^T dlogit. */
-int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
+int abacus_moe_router_wgrad(const void* x_TD, const void* dlogit_TK, const int32_t* idx_TK, int64_t T, int64_t D,
                             int64_t E, int64_t K, int dtype, float* partial_ws, void* dw_DE, void* stream);
 
 /* No counterpart in the reference: abacus_moe_router_wgrad for callers that cannot
@@ -191,16 +200,16 @@ int abacus_moe_router_wgrad(const void* x_TD, const float* dlogit_TK, const int3
  * dtype) is that need.  The array used is the one of the stream's device, which must be
  * the current device (a stream of another device is rejected (1); the null stream is the
  * current device's).  Calls that overlap on one GPU share that array and race. */
-int abacus_moe_router_wgrad_noalloc(const void* x_TD, const float* dlogit_TK, const int32_t* idx_TK, int64_t T,
+int abacus_moe_router_wgrad_noalloc(const void* x_TD, const void* dlogit_TK, const int32_t* idx_TK, int64_t T,
                                     int64_t D, int64_t E, int64_t K, int dtype, void* dw_DE, void* stream);
 
 /* Backward of router.py:49-51 and the sigmoid of :45 when Router.forward is
  * used on its own: dL/dweights -> dlogit_TK. */
-int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const float* score_TK, int64_t T,
-                             int64_t K, float route_scale, int dtype, float* dlogit_TK, void* stream);
+int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, const void* score_TK, int64_t T,
+                             int64_t K, double route_scale, int dtype, void* dlogit_TK, void* stream);
 
 /* Router.update_bias (router.py:57-70) for an explicit int64 index tensor. */
-int abacus_router_update_bias(const int64_t* indices_i64, int64_t N, int64_t E, float speed, int dtype,
+int abacus_router_update_bias(const int64_t* indices_i64, int64_t N, int64_t E, double speed, int dtype,
                               void* bias_E, void* stream);
 
 /* ---- auxiliary loss -------------------------------------------------------- */
@@ -214,13 +223,13 @@ int abacus_router_update_bias(const int64_t* indices_i64, int64_t N, int64_t E, 
  * caller to raise on, as torch.nn.functional.one_hot does; T must be > 0 (the
  * reference returns a zero without computing anything).  Deterministic. */
 int abacus_moe_load_balancing_fwd(const void* probs_TE, const int64_t* slots_TK, int64_t T, int64_t E, int64_t K,
-                                  float coeff_e, int dtype, void* ws, float* f_E, float* loss_f32, void* loss_out,
+                                  double coeff_e, int dtype, void* ws, float* f_E, float* loss_f32, void* loss_out,
                                   int32_t* bad_index, void* stream);
 
 /* Autograd of the above with respect to the probabilities: grad_probs[t, e] =
  * ((g * coeff_e) * f_E[e]) / T in fp32, rounded to `dtype`, g = the loss
  * gradient (one `dtype` element on the device). */
-int abacus_moe_load_balancing_bwd(const void* grad_loss, const float* f_E, int64_t T, int64_t E, float coeff_e,
+int abacus_moe_load_balancing_bwd(const void* grad_loss, const float* f_E, int64_t T, int64_t E, double coeff_e,
                                   int dtype, void* grad_probs_TE, void* stream);
 
 /* ---- the decoder around the MoE layer ---------------------------------------- */

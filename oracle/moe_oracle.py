@@ -87,7 +87,7 @@ def selection(scores: torch.Tensor, bias_E: torch.Tensor) -> torch.Tensor:
 
 def topk_canonical(sel: torch.Tensor, k: int) -> torch.Tensor:
     """Indices of the k largest values per row, descending; ties -> lower index; NaN first."""
-    v = sel.detach().to(torch.float32).cpu().numpy()
+    v = sel.detach().to(torch.float64).cpu().numpy()  # exact for every float dtype
     n = v.shape[-1]
     flat = v.reshape(-1, n)
     nan = np.isnan(flat)

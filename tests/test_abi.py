@@ -51,13 +51,13 @@ def test_host_library_exports_its_entry_points():
     assert len(_lib.HOST_SYMBOLS) >= 25
     for name in _lib.HOST_SYMBOLS:
         assert name in decls and hasattr(lib, name), name
-    assert _lib.load_host().abacus_moe_abi_version() == 4
+    assert _lib.load_host().abacus_moe_abi_version() == 5
     assert _lib.query("abacus_moe_hist_len", 4096, 8, device=torch.device("cpu")) == (4096 // 16) * 8
 
 
 def test_abi_version_and_queries():
     lib = _lib.load()
-    assert lib.abacus_moe_abi_version() == 4
+    assert lib.abacus_moe_abi_version() == 5
     assert _lib.query("abacus_moe_hist_len", 4096, 8) == (4096 // 16) * 8
     assert _lib.query("abacus_moe_hist_len", 17, 8) == 2 * 8
     # bf16 with at most 64 experts: the transposed weight, then fp32 partial logits
