@@ -141,17 +141,24 @@ def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
         return time.perf_counter() - t0
 
     # Sample size: a step of the reference algorithm costs a fixed part (its per-expert weight
-    # slices and their gradients) plus a part per token; both are fitted from 16 and 64 tokens,
-    # and the sample is the most tokens whose predicted step fits a third of the time budget.
+    # slices and their gradients) plus a part per token, both fitted from 16 and n2 tokens.  The
+    # sample is the most tokens whose predicted step fits a third of the time budget, raised (up to
+    # a 30 s step) until the per-token part is at least three quarters of the step, so the rate
+    # measures the per-token work the GPU is compared on rather than the fixed part.
     run(16)  # warm-up
-    t16, t64 = run(16), run(min(64, wl.tokens))
-    per_token = max((t64 - t16) / 48.0, 1e-7)
+    n2 = min(256, wl.tokens)
+    t16, tn2 = run(16), run(n2)
+    per_token = max((tn2 - t16) / max(n2 - 16, 1), 1e-7)
     fixed = max(t16 - 16 * per_token, 0.0)
-    tokens = int(min(wl.tokens, max(16, (target_seconds / 3 - fixed) / per_token)))
+    budget_tokens = (target_seconds / 3 - fixed) / per_token
+    dominant_tokens = min(3 * fixed / per_token, (30.0 - fixed) / per_token)
+    tokens = int(min(wl.tokens, max(16, budget_tokens, dominant_tokens)))
     times = [run(tokens)]
     while sum(times) < target_seconds and len(times) < 5:
         times.append(run(tokens))
     med = statistics.median(times)
+    share = tokens * per_token / (fixed + tokens * per_token)
+    full_step = fixed + wl.tokens * per_token
     cpu_model = platform.processor() or "unknown"
     try:
         with open("/proc/cpuinfo") as f:
@@ -166,11 +173,16 @@ def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
+        "fit": {"fixed_s_per_step": round(fixed, 4), "us_per_token": round(per_token * 1e6, 2),
+                "sample_tokens": tokens, "per_token_share_of_sample_step": round(share, 3),
+                "predicted_full_step_s": round(full_step, 3),
+                "predicted_full_step_tokens_per_s": round(wl.tokens / full_step, 1)},
         "sample": (f"{wl.name} layer (D={D}, E={wl.n_experts}, K={K}, M={wl.hidden}, "
                    f"{str(wl.dtype).replace('torch.', '')}, the benchmark's own weights) on the first {tokens} of its "
                    f"{wl.tokens} tokens, {'fwd+bwd' if wl.backward else 'fwd'} of the oracle's restatement of "
                    f"router.py:40-70 + moe.py:60-86, median of {len(times)} runs ({med:.2f} s each; fitted fixed "
-                   f"cost per step {fixed:.2f} s + {per_token * 1e6:.1f} us per token); torch CPU threads={cores}, "
+                   f"cost per step {fixed:.2f} s + {per_token * 1e6:.1f} us per token, the per-token part "
+                   f"{100 * share:.0f}% of the sample's step); torch CPU threads={cores}, "
                    f"os.cpu_count={os.cpu_count()}, cpu='{cpu_model}'"),
     }
 
