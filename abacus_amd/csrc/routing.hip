@@ -25,6 +25,11 @@ namespace abacus {
 constexpr int kRouteTB = 16;   // tokens per router / permute block (one MFMA row tile)
 constexpr int kMaxE = 256;     // experts handled by the fused router
 constexpr int kMaxK = 16;      // slots per token handled by the fused kernels
+// Limits of the routing entry points.  Beyond kMaxE experts or kMaxK slots the
+// router runs as a logits pass and a wave-per-token top-k pass, and the
+// dispatch and backward kernels take their 64-slot variants.
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxSlots = 64;
 constexpr int64_t kScanLdsBytes = 48 * 1024;  // route_scan stages histograms up to this size in LDS
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -105,6 +110,40 @@ __device__ inline uint64_t row16_max(uint64_t v) {
   return dpp_max_step<0xB1>(v);  // quad_perm [1, 0, 3, 2]
 }
 
+// The K rounds of top-k selection for one token whose selection keys L lanes
+// of a wave hold (lane ln: experts ln, ln + L, ..., CPL keys).  Each round
+// takes the maximum key over the token's lanes (a local maximum, the
+// row-of-16 maximum by DPP moves, and for L = 64 two lane shuffles) and
+// retires that expert.  Lane ln < K returns the ln-th pick (0 for a token
+// that is not valid).  L = 16 serves 4 tokens per wave at once; every lane of
+// the wave runs the same K rounds.
+template <int L, int CPL>
+__device__ __attribute__((always_inline)) inline int select_top_k(uint64_t (&key)[CPL], int K, int ln, bool valid) {
+  static_assert(L == 16 || L == 64, "a row of 16 lanes or the whole wave per token");
+  int my_e = 0;
+  for (int k = 0; k < K; ++k) {
+    uint64_t best = key[0];
+#pragma unroll
+    for (int c = 1; c < CPL; ++c) best = key[c] > best ? key[c] : best;
+    best = row16_max(best);
+    if constexpr (L == 64) {
+#pragma unroll
+      for (int off = 16; off < 64; off <<= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)best, off, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64);
+        const uint64_t o = ((uint64_t)hi << 32) | lo;
+        best = o > best ? o : best;
+      }
+    }
+    const int be = valid ? (int)(~(uint32_t)best) : 0;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      if (ln + L * c == be) key[c] = 0ull;
+    if (ln == k) my_e = be;
+  }
+  return my_e;
+}
+
 // ---------------------------------------------------------------------------
 // K1: fused router.  One block = 16 tokens x all experts; the NW waves split
 // the D reduction (k-blocks interleaved), partials are summed in LDS in a
@@ -126,7 +165,11 @@ __device__ inline uint64_t row16_max(uint64_t v) {
 //                   b and stores the fp32 partial logits at part[s][t][EP];
 //   kRouteFromPart  block b adds the kRouterSplit partials of its tokens in
 //                   slice order, then runs the epilogue (no MFMA).
-enum { kRouteFull = 0, kRoutePart = 1, kRouteFromPart = 2 };
+// and, for more experts or slots than the epilogue holds:
+//   kRouteLogits    block (b, g) computes the logits of token block b for
+//                   experts [g EP, (g + 1) EP) (rows of wt, zero past E) and
+//                   stores them rounded to T; router_topk_kernel routes.
+enum { kRouteFull = 0, kRoutePart = 1, kRouteFromPart = 2, kRouteLogits = 3 };
 constexpr int kRouterSplit = 8;
 template <typename T, int NF, bool WLDS, int NW, int MODE = kRouteFull>
 __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
@@ -142,11 +185,13 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
   constexpr int WROW = EP * 2;  // bytes of one staged w row
   constexpr int NTH = NW * 64;
   constexpr bool MMA = MODE != kRouteFromPart;
+  constexpr bool EPI = MODE == kRouteFull || MODE == kRouteFromPart;  // runs the top-k epilogue
+  static_assert(!(WLDS && MODE == kRouteLogits), "the logits pass reads the transposed copy");
   __shared__ float red[MMA ? NW : 1][kRouteTB][EP];
-  __shared__ float s_sc[kRouteTB][EP];
-  __shared__ float s_sel[kRouteTB][EP];
-  __shared__ int s_cnt[EP];
-  __shared__ float s_bias[EP];
+  __shared__ float s_sc[EPI ? kRouteTB : 1][EPI ? EP : 1];
+  __shared__ float s_sel[EPI ? kRouteTB : 1][EPI ? EP : 1];
+  __shared__ int s_cnt[EPI ? EP : 1];
+  __shared__ float s_bias[EPI ? EP : 1];
   __shared__ __align__(16) char s_w[WLDS ? NW : 1][WLDS ? 32 * WROW : 16];
 
   const int tid = threadIdx.x;
@@ -156,10 +201,15 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
   // this block's k range: one slice of DS (a multiple of the k-block) or all of D
   const int kbeg = MODE == kRoutePart ? (int)blockIdx.y * DS : 0;
   const int kend = MODE == kRoutePart ? min(D, kbeg + DS) : D;
-  for (int i = tid; i < EP; i += NTH) {
-    s_cnt[i] = 0;
-    // read here, used after the first barrier: the load overlaps the logits pass
-    if (MODE != kRoutePart) s_bias[i] = i < E ? to_f32<T>(bias[i]) : 0.f;
+  // the logits pass: this block's group of EP experts
+  const int e_base = MODE == kRouteLogits ? (int)blockIdx.y * EP : 0;
+  if constexpr (MODE == kRouteLogits) wt += (int64_t)e_base * D;
+  if constexpr (EPI) {
+    for (int i = tid; i < EP; i += NTH) {
+      s_cnt[i] = 0;
+      // read here, used after the first barrier: the load overlaps the logits pass
+      s_bias[i] = i < E ? to_f32<T>(bias[i]) : 0.f;
+    }
   }
 
   f32x4_t acc[NF];
@@ -268,6 +318,8 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
       a = zero16();
 #pragma unroll
       for (int f = 0; f < NF; ++f) b[f] = zero16();
+      // unrolled: constant element indexes keep a and b in registers
+#pragma unroll
       for (int i = 0; i < VEC; ++i) {
         if (k + i < D) {
           if (row_ok) VecTraits<T>::set(a, i, to_f32<T>(xrow[k + i]));
@@ -322,9 +374,9 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
     }
     if constexpr (MODE == kRoutePart) {
       if (t < T_) part[((int64_t)blockIdx.y * T_ + t) * EP + e] = l;
-      continue;
-    }
-    if (e < E && t < T_) {
+    } else if constexpr (MODE == kRouteLogits) {
+      if (e_base + e < E && t < T_) logits[(int64_t)t * E + e_base + e] = from_f32<T>(round_to<T>(l));
+    } else if (e < E && t < T_) {
       const float lr = round_to<T>(l);
       logits[(int64_t)t * E + e] = from_f32<T>(lr);
       const float s = round_to<T>(sigmoid_f32_cr(lr));
@@ -332,63 +384,101 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
       s_sel[tok][e] = round_to<T>(s + s_bias[e]);
     }
   }
-  if constexpr (MODE == kRoutePart) return;
-  __syncthreads();
+  if constexpr (EPI) {
+    __syncthreads();
 
-  // Top-K: L lanes per token, lane j of a token holding experts j, j + L, ...
-  // as selection keys.  Each of the K rounds takes the maximum key over the
-  // token's lanes (a local maximum, then the row-of-16 maximum by DPP moves,
-  // and for L = 64 two lane shuffles) and retires that expert; the picks'
-  // scores are read and summed after the rounds.  The rounds are a chain of
-  // dependent steps, so up to 64 experts a token gets 16 lanes (4 tokens per
-  // wave at once, a block's 16 tokens in one pass; with 64 lanes and a token
-  // per pass this epilogue took most of the kernel's ~28 us at small
-  // batches); beyond 64 experts, 64 lanes keep the keys per lane (and
-  // registers) few.
-  constexpr int L = EP <= 64 ? 16 : 64;
-  constexpr int TPW = 64 / L;                  // tokens per wave pass
-  constexpr int CPL = EP <= L ? 1 : EP / L;    // experts per lane
-  const int sub = lane / L, ln = lane % L;
-  for (int tok0 = wave * TPW; tok0 < kRouteTB; tok0 += NW * TPW) {
-    const int tok = tok0 + sub;
-    const int t = t0 + tok;
+    // Top-K: L lanes per token, lane j of a token holding experts j, j + L, ...
+    // as selection keys (select_top_k); the picks' scores are read and summed
+    // after the rounds.  The rounds are a chain of dependent steps, so up to 64
+    // experts a token gets 16 lanes (4 tokens per wave at once, a block's 16
+    // tokens in one pass; with 64 lanes and a token per pass this epilogue took
+    // most of the kernel's ~28 us at small batches); beyond 64 experts, 64 lanes
+    // keep the keys per lane (and registers) few.  K <= L (kMaxK = 16).
+    constexpr int L = EP <= 64 ? 16 : 64;
+    constexpr int TPW = 64 / L;                  // tokens per wave pass
+    constexpr int CPL = EP <= L ? 1 : EP / L;    // experts per lane
+    const int sub = lane / L, ln = lane % L;
+    for (int tok0 = wave * TPW; tok0 < kRouteTB; tok0 += NW * TPW) {
+      const int tok = tok0 + sub;
+      const int t = t0 + tok;
+      const bool valid = t < T_;
+      uint64_t key[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int e = ln + L * c;
+        key[c] = valid && e < E ? selection_key(s_sel[tok][e], e) : 0ull;
+      }
+      const int my_e = select_top_k<L, CPL>(key, K, ln, valid);  // lane k: the k-th pick
+      // (lanes past K, and invalid tokens, read a score they do not use)
+      const float my_s = s_sc[tok][my_e];
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) sum += __shfl(my_s, k, L);  // pick order
+      if (valid && ln < K) {
+        atomicAdd(&s_cnt[my_e], 1);
+        const float denom = round_to<T>(sum);
+        const float w = round_to<T>(round_to<T>(my_s / denom) * route_scale);
+        const int64_t o = (int64_t)t * K + ln;
+        weights[o] = from_f32<T>(w);
+        indices[o] = my_e;
+        idx32[o] = my_e;
+        score[o] = my_s;
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += NTH) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K1b: routing from stored logits, for up to kMaxExperts experts and
+// kMaxSlots slots (the kRouteLogits pass wrote them).  One block per 16
+// tokens (the histogram block of the scan and the gather), a wave per token:
+// lane l rebuilds the selection values of experts l, l + 64, ... from the
+// logits exactly as the fused epilogue does (the stored logit is the rounded
+// one, so score and selection value are the same bits), select_top_k picks K
+// of them, and lane k writes the k-th pick, rereading its logit for the score.
+// ---------------------------------------------------------------------------
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) void router_topk_kernel(const T* __restrict__ logits, const T* __restrict__ bias,
+                                                          int T_, int E, int K, float route_scale,
+                                                          T* __restrict__ weights, int64_t* __restrict__ indices,
+                                                          int32_t* __restrict__ idx32, float* __restrict__ score,
+                                                          int32_t* __restrict__ hist) {
+  static_assert(CPL * 64 <= kMaxExperts, "the block's histogram");
+  __shared__ int s_cnt[CPL * 64];
+  __shared__ float s_bias[CPL * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < CPL * 64; e += 256) {
+    s_cnt[e] = 0;
+    s_bias[e] = e < E ? to_f32<T>(bias[e]) : 0.f;
+  }
+  __syncthreads();
+  for (int tok = wave; tok < kRouteTB; tok += 4) {
+    const int t = (int)blockIdx.x * kRouteTB + tok;
     const bool valid = t < T_;
+    const T* row = logits + (int64_t)(valid ? t : 0) * E;
+    float lg[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int e = lane + 64 * c;
+      lg[c] = valid && e < E ? to_f32<T>(row[e]) : 0.f;
+    }
     uint64_t key[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
-      const int e = ln + L * c;
-      key[c] = valid && e < E ? selection_key(s_sel[tok][e], e) : 0ull;
+      const int e = lane + 64 * c;
+      const float s = round_to<T>(sigmoid_f32_cr(lg[c]));
+      key[c] = valid && e < E ? selection_key(round_to<T>(s + s_bias[e]), e) : 0ull;
     }
-    int my_e = 0;  // lane k: the k-th pick
-    for (int k = 0; k < K; ++k) {
-      uint64_t best = key[0];
-#pragma unroll
-      for (int c = 1; c < CPL; ++c) best = key[c] > best ? key[c] : best;
-      best = row16_max(best);
-      if constexpr (L == 64) {
-#pragma unroll
-        for (int off = 16; off < 64; off <<= 1) {
-          const uint32_t lo = __shfl_xor((uint32_t)best, off, 64);
-          const uint32_t hi = __shfl_xor((uint32_t)(best >> 32), off, 64);
-          const uint64_t o = ((uint64_t)hi << 32) | lo;
-          best = o > best ? o : best;
-        }
-      }
-      const int be = valid ? (int)(~(uint32_t)best) : 0;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c)
-        if (ln + L * c == be) key[c] = 0ull;
-      if (ln == k) my_e = be;
-    }
-    // (lanes past K, and invalid tokens, read a score they do not use)
-    const float my_s = s_sc[tok][my_e];
+    const int my_e = select_top_k<64, CPL>(key, K, lane, valid);
+    const float my_s = valid && lane < K ? round_to<T>(sigmoid_f32_cr(to_f32<T>(row[my_e]))) : 0.f;
     float sum = 0.f;
-    for (int k = 0; k < K; ++k) sum += __shfl(my_s, k, L);  // pick order
-    if (valid && ln < K) {
+    for (int k = 0; k < K; ++k) sum += __shfl(my_s, k, 64);  // pick order
+    if (valid && lane < K) {
       atomicAdd(&s_cnt[my_e], 1);
       const float denom = round_to<T>(sum);
       const float w = round_to<T>(round_to<T>(my_s / denom) * route_scale);
-      const int64_t o = (int64_t)t * K + ln;
+      const int64_t o = (int64_t)t * K + lane;
       weights[o] = from_f32<T>(w);
       indices[o] = my_e;
       idx32[o] = my_e;
@@ -396,7 +486,7 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
     }
   }
   __syncthreads();
-  for (int e = tid; e < E; e += NTH) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+  for (int e = tid; e < E; e += 256) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
 }
 
 // ---------------------------------------------------------------------------
@@ -422,16 +512,17 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
   }
   auto hv = [&](int b, int e) -> int { return STAGED ? s_hist[b * E + e] : hist[(int64_t)b * E + e]; };
   // 16 groups of 64 threads; group q sums blocks b0 .. b1-1, lane l experts l, l + 64, ...
-  __shared__ int part[16][kMaxE];
-  __shared__ int cnt[kMaxE];
-  __shared__ int off[kMaxE + 1];
+  __shared__ int part[16][kMaxExperts];
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int off[kMaxExperts + 1];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int q = tid >> 6;
   const int per = (nb + 15) / 16;
   const int b0 = q * per;
   const int b1 = min(nb, b0 + per);
-  for (int e = lane; e < kMaxE; e += 64) {
+  const int E64 = (E + 63) / 64 * 64;  // whole waves of experts (<= 1024 threads)
+  for (int e = lane; e < E64; e += 64) {
     int p = 0;
     if (e < E)
 #pragma unroll 16
@@ -439,11 +530,11 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(const int32_t* __restr
     part[q][e] = p;
   }
   __syncthreads();
-  // counts, then their exclusive scan over experts: 4 waves of 64, a wave
-  // scan by lane shuffles plus the earlier waves' totals
-  __shared__ int wtot[kMaxE / 64];
+  // counts, then their exclusive scan over experts: a wave of 64 experts per
+  // 64 threads, a wave scan by lane shuffles plus the earlier waves' totals
+  __shared__ int wtot[kMaxExperts / 64];
   int c = 0, incl = 0;
-  if (tid < kMaxE) {
+  if (tid < E64) {
     for (int i = 0; i < 16; ++i) c += part[i][tid];
     cnt[tid] = c;
     incl = tid < E ? c : 0;
@@ -505,7 +596,7 @@ constexpr int kFusedScanInts = 4096;
 // stages the histograms in LDS and derives the expert counts, offsets and its
 // own block's first rows (the sums route_scan_kernel makes); block (0, 0) also
 // writes counts and offsets and applies the bias step (bias non-NULL).
-template <typename T, bool SCAN>
+template <typename T, bool SCAN, int KM>
 __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict__ x, const int32_t* __restrict__ idx,
                                                              const int32_t* __restrict__ base, int T_, int D, int E,
                                                              int K, int32_t* __restrict__ pos,
@@ -516,11 +607,13 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
                                                              int32_t* __restrict__ offsets) {
   constexpr int VEC = VecTraits<T>::kN;
   constexpr int U = kPermuteBatch;
-  static_assert(kRouteTB * kMaxK == 256, "one thread per (token, slot) entry of s_e");
-  static_assert(kMaxE == 256, "one thread per expert in the scan");
-  static_assert(kMaxK % 4 == 0, "a token's slots as 16-byte vectors");
-  __shared__ __align__(16) int s_e[kRouteTB][kMaxK];  // -1 past K and past the batch
-  __shared__ int s_pos[kRouteTB][kMaxK];
+  // KM: slot capacity, kMaxK or kMaxSlots; EPT (token, slot) entries of s_e per thread
+  constexpr int EPT = kRouteTB * KM / 256;
+  static_assert(kRouteTB * KM % 256 == 0, "whole entries per thread");
+  static_assert(!SCAN || (KM == kMaxK && EPT == 1 && kMaxE == 256), "the fused scan: one thread per expert");
+  static_assert(KM % 4 == 0, "a token's slots as 16-byte vectors");
+  __shared__ __align__(16) int s_e[kRouteTB][KM];  // -1 past K and past the batch
+  __shared__ int s_pos[kRouteTB][KM];
   __shared__ int s_h[SCAN ? kFusedScanInts : 1];
   __shared__ int s_all[SCAN ? 256 : 1], s_prev[SCAN ? 256 : 1], s_base[SCAN ? kMaxE : 1];
   __shared__ int s_wtot[4];
@@ -529,11 +622,15 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
   const bool writer = blockIdx.y == 0;
   const int ntok = min(kRouteTB, T_ - t0);
   // Loads that need no routing go first and are in flight during the scan:
-  // this block's slots (thread t: token t / kMaxK, slot t % kMaxK) and its
-  // first batch of x vectors (tokens t0.., columns c0 .. c0 + ncol of this
+  // this block's slots (entry i = tid + 256 j: token i / KM, slot i % KM) and
+  // its first batch of x vectors (tokens t0.., columns c0 .. c0 + ncol of this
   // block's chunk).
-  int my_e = -1;
-  if (tid % kMaxK < K && tid / kMaxK < ntok) my_e = idx[(int64_t)(t0 + tid / kMaxK) * K + tid % kMaxK];
+  int my_e[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + 256 * j;
+    my_e[j] = i % KM < K && i / KM < ntok ? idx[(int64_t)(t0 + i / KM) * K + i % KM] : -1;
+  }
   const int nvec = D / VEC;
   const int per = (nvec + gridDim.y - 1) / gridDim.y;  // columns of this chunk
   const int c0 = blockIdx.y * per;
@@ -617,25 +714,32 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
     }
     __syncthreads();
   }
-  if (tid < kRouteTB * kMaxK) s_e[tid / kMaxK][tid % kMaxK] = my_e;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int i = tid + 256 * j;
+    s_e[i / KM][i % KM] = my_e[j];
+  }
   __syncthreads();
-  if (tid < ntok * K) {
-    const int tok = tid / K, k = tid % K;
+  // RB earlier tokens' rows per batch of 16-byte reads (two 16-slot rows, or
+  // one 64-slot row)
+  constexpr int RB = KM <= 16 ? 2 : 1;
+  for (int i = tid; i < ntok * K; i += 256) {
+    const int tok = i / K, k = i % K;
     const int e = s_e[tok][k];
     // rank = earlier tokens' slots holding e (a token's own K experts are
-    // distinct), two tokens' rows per batch as 16-byte reads all in flight
+    // distinct), a batch of rows as 16-byte reads all in flight
     int rank = 0;
-    for (int t2 = 0; t2 < tok; t2 += 2) {
-      int4 v[2][kMaxK / 4];
+    for (int t2 = 0; t2 < tok; t2 += RB) {
+      int4 v[RB][KM / 4];
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < RB; ++a)
 #pragma unroll
-        for (int q = 0; q < kMaxK / 4; ++q)
+        for (int q = 0; q < KM / 4; ++q)
           v[a][q] = t2 + a < tok ? *reinterpret_cast<const int4*>(&s_e[t2 + a][4 * q]) : make_int4(-1, -1, -1, -1);
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < RB; ++a)
 #pragma unroll
-        for (int q = 0; q < kMaxK / 4; ++q)
+        for (int q = 0; q < KM / 4; ++q)
           rank += (v[a][q].x == e) + (v[a][q].y == e) + (v[a][q].z == e) + (v[a][q].w == e);
     }
     const int p = (SCAN ? s_base[e] : base[(int64_t)blockIdx.x * E + e]) + rank;
@@ -658,7 +762,7 @@ __global__ __launch_bounds__(256) void permute_gather_kernel(const T* __restrict
 }
 
 // Sort a token's K slots by expert index so sums run in the reference's
-// ascending-expert order (moe.py:72,85).  Runs on one thread; K <= kMaxK.
+// ascending-expert order (moe.py:72,85).  Runs on one thread; K <= kMaxSlots.
 __device__ inline void sort_slots_by_expert(int K, int* e, int* p, float* w) {
   for (int i = 1; i < K; ++i) {
     int ke = e[i], kp = p[i];
@@ -916,23 +1020,112 @@ __global__ __launch_bounds__(256) void combine_bwd_kernel(const T* __restrict__ 
   }
 }
 
+// combine_bwd_kernel for K > kMaxK (up to kMaxSlots): lane k holds slot k's
+// row, weight and score; the token's row of dout is read once per group of
+// kMaxK slots, each group's dot products summed as in combine_bwd_kernel (the
+// same per-lane order and butterfly), and the gating sums of gating_bwd_token
+// run in slot order through lane shuffles.
+template <typename T>
+__global__ __launch_bounds__(256) void combine_bwd_wide_kernel(const T* __restrict__ dout, const T* __restrict__ y,
+                                                               const T* __restrict__ weights,
+                                                               const float* __restrict__ score,
+                                                               const int32_t* __restrict__ pos, int T_, int D, int K,
+                                                               float rho, T* __restrict__ dy,
+                                                               float* __restrict__ dlogit) {
+  constexpr int VEC = VecTraits<T>::kN;
+  constexpr int U = kGatherBatch;
+  constexpr int G = kMaxK;
+  const int lane = threadIdx.x & 63;
+  const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (t >= T_) return;
+  const bool on = lane < K;
+  const int my_p = on ? pos[(int64_t)t * K + lane] : 0;
+  const float my_w = on ? to_f32<T>(weights[(int64_t)t * K + lane]) : 0.f;
+  const float my_s = on ? score[(int64_t)t * K + lane] : 0.f;
+  float my_dw = 0.f;
+  const int nvec = D / VEC;
+  for (int k0 = 0; k0 < K; k0 += G) {
+    const int nk = min(G, K - k0);
+    int p[G];
+    float w[G], dw[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      p[j] = __shfl(my_p, k0 + j, 64);
+      w[j] = __shfl(my_w, k0 + j, 64);
+      dw[j] = 0.f;
+    }
+    for (int c0 = 0; c0 < nvec; c0 += 64 * U) {
+      Vec16 g[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = c0 + u * 64 + lane;
+        g[u] = c < nvec ? ld16(dout + (int64_t)t * D + c * VEC) : zero16();
+      }
+#pragma unroll
+      for (int j = 0; j < G; ++j) {
+        if (j >= nk) break;
+        Vec16 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = c0 + u * 64 + lane;
+          v[u] = c < nvec ? ld16(y + (int64_t)p[j] * D + c * VEC) : zero16();
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int c = c0 + u * 64 + lane;
+          if (c >= nvec) continue;
+          Vec16 o;
+          float part = 0.f;
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) {
+            const float gi = VecTraits<T>::get(g[u], i);
+            part += gi * VecTraits<T>::get(v[u], i);
+            VecTraits<T>::set(o, i, gi * w[j]);
+          }
+          dw[j] += part;
+          st16(dy + (int64_t)p[j] * D + c * VEC, o);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      if (j < nk) {
+        const float s = wave_sum(dw[j]);
+        if (lane == k0 + j) my_dw = s;
+      }
+  }
+  float sum = 0.f, c = 0.f;
+  for (int k = 0; k < K; ++k) {
+    sum += __shfl(my_s, k, 64);
+    c += __shfl(my_dw, k, 64) * __shfl(my_w, k, 64);
+  }
+  if (on) {
+    const float ds = (rho * my_dw - c) / round_to<T>(sum);
+    dlogit[(int64_t)t * K + lane] = ds * my_s * (1.0f - my_s);
+  }
+}
+
 // Standalone router backward (Router.forward used on its own): dweights -> dlogit.
+// The sums of gating_bwd_token in its order, reading the token's slots twice
+// instead of holding them (any K).
 template <typename T>
 __global__ void router_gating_bwd_kernel(const T* __restrict__ dweights, const T* __restrict__ weights,
                                          const float* __restrict__ score, int T_, int K, float rho,
                                          float* __restrict__ dlogit) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= T_) return;
-  float dw[kMaxK], w[kMaxK], s[kMaxK], dl[kMaxK];
-  float sum = 0.f;
+  const int64_t o = (int64_t)t * K;
+  float sum = 0.f, c = 0.f;
   for (int k = 0; k < K; ++k) {
-    dw[k] = to_f32<T>(dweights[(int64_t)t * K + k]);
-    w[k] = to_f32<T>(weights[(int64_t)t * K + k]);
-    s[k] = score[(int64_t)t * K + k];
-    sum += s[k];
+    sum += score[o + k];
+    c += to_f32<T>(dweights[o + k]) * to_f32<T>(weights[o + k]);
   }
-  gating_bwd_token(K, rho, dw, w, s, round_to<T>(sum), dl);
-  for (int k = 0; k < K; ++k) dlogit[(int64_t)t * K + k] = dl[k];
+  const float denom = round_to<T>(sum);
+  for (int k = 0; k < K; ++k) {
+    const float s = score[o + k];
+    const float ds = (rho * to_f32<T>(dweights[o + k]) - c) / denom;
+    dlogit[o + k] = ds * s * (1.0f - s);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -949,26 +1142,19 @@ __global__ __launch_bounds__(256) void unpermute_bwd_kernel(const T* __restrict_
                                                             const T* __restrict__ wt, int T_, int D, int K,
                                                             T* __restrict__ dx) {
   constexpr int VEC = VecTraits<T>::kN;
-  __shared__ int s_p[kMaxK];
-  __shared__ int s_e[kMaxK];
-  __shared__ float s_dl[kMaxK];
+  __shared__ int s_p[kMaxSlots];
+  __shared__ int s_e[kMaxSlots];
+  __shared__ float s_dl[kMaxSlots];
   const int tid = threadIdx.x;
   const int nvec = D / VEC;
   for (int t = blockIdx.x; t < T_; t += gridDim.x) {
-    if (tid == 0) {
-      int e[kMaxK], p[kMaxK];
-      float dl[kMaxK];
+    if (tid == 0) {  // the token's slots, sorted in place in LDS
       for (int k = 0; k < K; ++k) {
-        e[k] = idx[(int64_t)t * K + k];
-        p[k] = dxp ? pos[(int64_t)t * K + k] : 0;
-        dl[k] = dlogit[(int64_t)t * K + k];
+        s_e[k] = idx[(int64_t)t * K + k];
+        s_p[k] = dxp ? pos[(int64_t)t * K + k] : 0;
+        s_dl[k] = dlogit[(int64_t)t * K + k];
       }
-      sort_slots_by_expert(K, e, p, dl);
-      for (int k = 0; k < K; ++k) {
-        s_e[k] = e[k];
-        s_p[k] = p[k];
-        s_dl[k] = dl[k];
-      }
+      sort_slots_by_expert(K, s_e, s_p, s_dl);
     }
     __syncthreads();
     if (D % VEC != 0) {
@@ -1176,6 +1362,7 @@ __device__ inline Vec16 frag_c(const char* cs, int f0, int ks, int lane) {
 }
 }  // namespace rwg
 
+template <int KM>  // slot capacity: kMaxK or kMaxSlots
 __global__ __launch_bounds__(256) void router_wgrad_mfma_kernel(const uint16_t* __restrict__ x,
                                                                 const float* __restrict__ dlogit,
                                                                 const int32_t* __restrict__ idx, int T_, int D,
@@ -1192,7 +1379,7 @@ __global__ __launch_bounds__(256) void router_wgrad_mfma_kernel(const uint16_t* 
   // A stage's x chunks and its (expert, dlogit) pairs are loaded together, two
   // stages ahead, so building C^T waits on no global load (reading the pairs in
   // the stage itself put a memory round trip in every stage).
-  constexpr int PP = (TS * kMaxK + 255) / 256;  // pairs per thread per stage
+  constexpr int PP = (TS * KM + 255) / 256;  // pairs per thread per stage
   Vec16 xr[PF][XV];
   int pe[PF][PP];
   float pd[PF][PP];
@@ -1454,9 +1641,9 @@ __global__ void router_wgrad_reduce_kernel(const float* __restrict__ partial, in
 template <typename T>
 __global__ __launch_bounds__(1024) void update_bias_kernel(const int64_t* __restrict__ indices, int64_t N, int E,
                                                            float speed, T* __restrict__ bias) {
-  __shared__ int cnt[kMaxE];
+  __shared__ int cnt[kMaxExperts];
   const int tid = threadIdx.x;
-  if (tid < kMaxE) cnt[tid] = 0;
+  if (tid < kMaxExperts) cnt[tid] = 0;
   __syncthreads();
   for (int64_t i = tid; i < N; i += blockDim.x) {
     const int64_t e = indices[i];
@@ -1492,9 +1679,10 @@ int check_dtype(int dtype) {
 int check_route_shape(int64_t T, int64_t D, int64_t E, int64_t K, int dtype, bool need_vec = true) {
   if (check_dtype(dtype)) return 1;
   ABACUS_CHECK_ARG(T >= 0 && T < (1ll << 31), "token count %lld out of range", (long long)T);
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
-  ABACUS_CHECK_ARG(K >= 1 && K <= E && K <= kMaxK, "top_k %lld: must be in [1, min(n_experts, %d)]",
-                   (long long)K, kMaxK);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxExperts, "n_experts %lld: supported range 1..%d", (long long)E,
+                   kMaxExperts);
+  ABACUS_CHECK_ARG(K >= 1 && K <= E && K <= kMaxSlots, "top_k %lld: must be in [1, min(n_experts, %d)]",
+                   (long long)K, kMaxSlots);
   ABACUS_CHECK_ARG(D >= 1 && D < (1ll << 31), "dim %lld out of range", (long long)D);
   ABACUS_CHECK_ARG(!need_vec || D % vec_elems(dtype) == 0,
                    "dim %lld must be a multiple of %d for this dtype", (long long)D, vec_elems(dtype));
@@ -1512,10 +1700,16 @@ void launch_transpose(const void* w, void* wt, int D, int E, int E_pad, hipStrea
 
 // Experts of the router kernel instance for E (a multiple of 16: 16, 32, 48,
 // 64, 128 or 256): the rows of the transposed router weights, zero beyond E.
+// Rows of the transposed router weight: E rounded up to the expert count of
+// the router kernel instance (16 .. 64 by 16, 128, 256, then whole groups of
+// 256 for the logits pass).
 inline int e_pad(int64_t E) {
   const int p = (int)((E + 15) / 16) * 16;
-  return p <= 64 ? p : (p <= 128 ? 128 : 256);
+  return p <= 64 ? p : (p <= 128 ? 128 : (int)((p + 255) / 256 * 256));
 }
+// More experts or slots than the fused router's epilogue holds: the logits
+// pass and router_topk_kernel.
+inline bool wide_routing(int64_t E, int64_t K) { return E > kMaxE || K > kMaxK; }
 
 // The router workspace: the transposed weight (e_pad(E), D), then, for the
 // split router, the fp32 partial logits (kRouterSplit, T, e_pad(E)) of up to
@@ -1593,7 +1787,10 @@ inline unsigned gather_ysplit(int64_t nb, int64_t nvec) {
 }
 
 // Calls f(std::integral_constant<int, KB>) with KB = K rounded up to 1, 2, 4,
-// 8 or 16: the slot bound of the wave-per-token gather kernels.
+// 8 or 16: the slot bound of the wave-per-token gather kernels.  Past 8 slots
+// for_each_sorted_slot keeps a slot per lane, so KB = 16 serves every K up to
+// kMaxSlots there; combine_bwd_kernel holds KB slots in registers and takes
+// K <= kMaxK only (combine_bwd_wide_kernel beyond).
 template <typename F>
 void with_slot_bound(int64_t K, F&& f) {
   if (K <= 1) f(std::integral_constant<int, 1>());
@@ -1623,6 +1820,57 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   hipStream_t s = (hipStream_t)stream;
   const int EP = e_pad(E);
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
+  if (wide_routing(E, K)) {
+    // the logits pass over groups of up to 256 experts, then the top-k pass
+    if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    ABACUS_CHECK_LAUNCH("router weight transpose");
+    if (nb == 0) return 0;
+    const int group = std::min(EP, 256);
+    const dim3 lgrid((unsigned)nb, (unsigned)(EP / group));
+#define ROUTER_LOGITS(TT, NF)                                                                                       \
+  hipLaunchKernelGGL((router_fwd_kernel<TT, NF, false, 4, kRouteLogits>), lgrid, dim3(256), 0, s, (const TT*)x_TD, \
+                     (const TT*)wt_ws, (const TT*)nullptr, (TT*)nullptr, (const TT*)bias_E, (int)T, (int)D, (int)E,  \
+                     (int)K, route_scale, (TT*)logits_TE, (TT*)nullptr, (int64_t*)nullptr, (int32_t*)nullptr,        \
+                     (float*)nullptr, (int32_t*)nullptr, (float*)nullptr, 0)
+#define ROUTER_LOGITS_NF(TT)               \
+  switch (group / 16) {                    \
+    case 1: ROUTER_LOGITS(TT, 1); break;   \
+    case 2: ROUTER_LOGITS(TT, 2); break;   \
+    case 3: ROUTER_LOGITS(TT, 3); break;   \
+    case 4: ROUTER_LOGITS(TT, 4); break;   \
+    case 8: ROUTER_LOGITS(TT, 8); break;   \
+    default: ROUTER_LOGITS(TT, 16); break; \
+  }
+    if (dtype == kBF16) {
+      ROUTER_LOGITS_NF(uint16_t)
+    } else {
+      ROUTER_LOGITS_NF(float)
+    }
+#undef ROUTER_LOGITS_NF
+#undef ROUTER_LOGITS
+    ABACUS_CHECK_LAUNCH("router logits");
+    const int64_t cpl = (E + 63) / 64;  // selection keys per lane
+#define ROUTER_TOPK(TT, CPL)                                                                                          \
+  hipLaunchKernelGGL((router_topk_kernel<TT, CPL>), dim3(nb), dim3(256), 0, s, (const TT*)logits_TE,                \
+                     (const TT*)bias_E, (int)T, (int)E, (int)K, route_scale, (TT*)weights_TK, indices_TK, idx_TK, \
+                     score_TK, hist)
+#define ROUTER_TOPK_CPL(TT)                   \
+  if (cpl <= 1) ROUTER_TOPK(TT, 1);           \
+  else if (cpl <= 2) ROUTER_TOPK(TT, 2);      \
+  else if (cpl <= 4) ROUTER_TOPK(TT, 4);      \
+  else if (cpl <= 8) ROUTER_TOPK(TT, 8);      \
+  else ROUTER_TOPK(TT, 16);
+    if (dtype == kBF16) {
+      ROUTER_TOPK_CPL(uint16_t)
+    } else {
+      ROUTER_TOPK_CPL(float)
+    }
+#undef ROUTER_TOPK_CPL
+#undef ROUTER_TOPK
+    ABACUS_CHECK_LAUNCH("router top-k");
+    return 0;
+  }
   // bf16 with whole 16-byte rows of w_DE and x: the router reads w_DE itself
   // and its block 0 writes the transposed copy (for the backward) as it goes.
   const bool wlds = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && EP <= 64 && nb > 0;
@@ -1694,7 +1942,8 @@ int abacus_moe_route_scan(const int32_t* hist, int64_t T, int64_t E, int64_t K, 
                           int32_t* offsets_E1, void* stream) {
   const float bias_update_speed = (float)bias_update_speed_d;
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxExperts, "n_experts %lld: supported range 1..%d", (long long)E,
+                   kMaxExperts);
   ABACUS_CHECK_ARG(T >= 0 && T * K < (1ll << 31), "bad token count %lld", (long long)T);
   hipStream_t s = (hipStream_t)stream;
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
@@ -1723,14 +1972,19 @@ int abacus_moe_permute_gather(const void* x_TD, const int32_t* idx_TK, const int
   if (nb == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)nb, gather_ysplit(nb, D / vec_elems(dtype)));
-  if (dtype == kBF16)
-    hipLaunchKernelGGL((permute_gather_kernel<uint16_t, false>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
-                       base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, nullptr, nullptr,
-                       0.f, nullptr, nullptr);
-  else
-    hipLaunchKernelGGL((permute_gather_kernel<float, false>), grid, dim3(256), 0, s, (const float*)x_TD, idx_TK, base,
-                       (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD, nullptr, nullptr, 0.f,
-                       nullptr, nullptr);
+  auto launch = [&](auto km) {
+    constexpr int KM = decltype(km)::value;
+    if (dtype == kBF16)
+      hipLaunchKernelGGL((permute_gather_kernel<uint16_t, false, KM>), grid, dim3(256), 0, s, (const uint16_t*)x_TD,
+                         idx_TK, base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, nullptr,
+                         nullptr, 0.f, nullptr, nullptr);
+    else
+      hipLaunchKernelGGL((permute_gather_kernel<float, false, KM>), grid, dim3(256), 0, s, (const float*)x_TD, idx_TK,
+                         base, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD, nullptr, nullptr,
+                         0.f, nullptr, nullptr);
+  };
+  if (K <= kMaxK) launch(std::integral_constant<int, kMaxK>());
+  else launch(std::integral_constant<int, kMaxSlots>());
   ABACUS_CHECK_LAUNCH("permute_gather");
   return 0;
 }
@@ -1742,7 +1996,9 @@ int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* id
   const float bias_update_speed = (float)bias_update_speed_d;
   if (check_route_shape(T, D, E, K, dtype)) return 1;
   const int64_t nb = (T + kRouteTB - 1) / kRouteTB;
-  if (nb * E > kFusedScanInts) {  // the scan as its own launch, then the gather
+  // the scan as its own launch, then the gather: large histograms, and the
+  // expert and slot counts past the fused scan's thread per expert and entry
+  if (nb * E > kFusedScanInts || wide_routing(E, K)) {
     if (abacus_moe_route_scan(hist, T, E, K, bias_E, bias_update_speed, dtype, base_ws, counts_E, offsets_E1, stream))
       return 1;
     return abacus_moe_permute_gather(x_TD, idx_TK, base_ws, T, D, E, K, dtype, pos_TK, perm_R, x_perm_RD, stream);
@@ -1753,11 +2009,11 @@ int abacus_moe_dispatch(const int32_t* hist, const void* x_TD, const int32_t* id
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)nb, gather_ysplit(nb, D / vec_elems(dtype)));
   if (dtype == kBF16)
-    hipLaunchKernelGGL((permute_gather_kernel<uint16_t, true>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
+    hipLaunchKernelGGL((permute_gather_kernel<uint16_t, true, kMaxK>), grid, dim3(256), 0, s, (const uint16_t*)x_TD, idx_TK,
                        nullptr, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (uint16_t*)x_perm_RD, hist,
                        (uint16_t*)bias_E, bias_update_speed, counts_E, offsets_E1);
   else
-    hipLaunchKernelGGL((permute_gather_kernel<float, true>), grid, dim3(256), 0, s, (const float*)x_TD, idx_TK,
+    hipLaunchKernelGGL((permute_gather_kernel<float, true, kMaxK>), grid, dim3(256), 0, s, (const float*)x_TD, idx_TK,
                        nullptr, (int)T, (int)D, (int)E, (int)K, pos_TK, perm_R, (float*)x_perm_RD, hist,
                        (float*)bias_E, bias_update_speed, counts_E, offsets_E1);
   ABACUS_CHECK_LAUNCH("dispatch");
@@ -1805,6 +2061,18 @@ int abacus_moe_combine_bwd(const void* dout_TD, const void* y_RD, const void* we
   hipStream_t s = (hipStream_t)stream;
   ABACUS_CHECK_ARG(T <= (int64_t)INT_MAX - 3, "too many tokens (%lld)", (long long)T);
   const unsigned grid = (unsigned)((T + 3) / 4);  // a token per wave
+  if (K > kMaxK) {
+    if (dtype == kBF16)
+      hipLaunchKernelGGL(combine_bwd_wide_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)dout_TD,
+                         (const uint16_t*)y_RD, (const uint16_t*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
+                         route_scale, (uint16_t*)dy_RD, dlogit_TK);
+    else
+      hipLaunchKernelGGL(combine_bwd_wide_kernel<float>, dim3(grid), dim3(256), 0, s, (const float*)dout_TD,
+                         (const float*)y_RD, (const float*)weights_TK, score_TK, pos_TK, (int)T, (int)D, (int)K,
+                         route_scale, (float*)dy_RD, dlogit_TK);
+    ABACUS_CHECK_LAUNCH("combine_bwd");
+    return 0;
+  }
   with_slot_bound(K, [&](auto kb) {
     constexpr int KB = decltype(kb)::value;
     if (dtype == kBF16)
@@ -1826,7 +2094,7 @@ int abacus_router_gating_bwd(const void* dweights_TK, const void* weights_TK, co
   float* dlogit_TK = (float*)dlogit_ws;
   const float route_scale = (float)route_scale_d;
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(K >= 1 && K <= kMaxK, "top_k %lld: supported range 1..%d", (long long)K, kMaxK);
+  ABACUS_CHECK_ARG(K >= 1 && K <= kMaxSlots, "top_k %lld: supported range 1..%d", (long long)K, kMaxSlots);
   if (T == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   const int grid = (int)((T + 255) / 256);
@@ -1941,8 +2209,12 @@ static int router_wgrad_launch(const WgradPlan& plan, const void* x_TD, const fl
   // With T == 0 the partial kernel visits no tokens and writes zero partials.
   if (path == 2) {
     const dim3 g1((unsigned)((D + rwg::TD - 1) / rwg::TD), (unsigned)nchunks, (unsigned)((E + rwg::TE - 1) / rwg::TE));
-    hipLaunchKernelGGL(router_wgrad_mfma_kernel, g1, dim3(256), 0, s, (const uint16_t*)x_TD, dlogit_TK, idx_TK,
-                       (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
+    if (K <= kMaxK)
+      hipLaunchKernelGGL(router_wgrad_mfma_kernel<kMaxK>, g1, dim3(256), 0, s, (const uint16_t*)x_TD, dlogit_TK,
+                         idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
+    else
+      hipLaunchKernelGGL(router_wgrad_mfma_kernel<kMaxSlots>, g1, dim3(256), 0, s, (const uint16_t*)x_TD, dlogit_TK,
+                         idx_TK, (int)T, (int)D, (int)E, (int)K, chunk, partial_ws);
   } else if (path == 0) {
     const int cols = 64 * wgrad_cpt(dtype);
     const dim3 g1((unsigned)((D + cols - 1) / cols), (unsigned)nchunks);
@@ -1986,8 +2258,10 @@ static int router_wgrad_launch(const WgradPlan& plan, const void* x_TD, const fl
 
 static int check_router_wgrad(int64_t E, int64_t K, int dtype) {
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
-  ABACUS_CHECK_ARG(K >= 1 && K <= E, "bad top_k %lld", (long long)K);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxExperts, "n_experts %lld: supported range 1..%d", (long long)E,
+                   kMaxExperts);
+  ABACUS_CHECK_ARG(K >= 1 && K <= E && K <= kMaxSlots, "top_k %lld: must be in [1, min(n_experts, %d)]",
+                   (long long)K, kMaxSlots);
   return 0;
 }
 
@@ -2019,7 +2293,8 @@ int abacus_router_update_bias(const int64_t* indices, int64_t N, int64_t E, doub
                               void* stream) {
   const float speed = (float)speed_d;
   if (check_dtype(dtype)) return 1;
-  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxE, "n_experts %lld: supported range 1..%d", (long long)E, kMaxE);
+  ABACUS_CHECK_ARG(E >= 1 && E <= kMaxExperts, "n_experts %lld: supported range 1..%d", (long long)E,
+                   kMaxExperts);
   hipStream_t s = (hipStream_t)stream;
   if (dtype == kBF16)
     hipLaunchKernelGGL(update_bias_kernel<uint16_t>, dim3(1), dim3(1024), 0, s, indices, N, (int)E, speed,

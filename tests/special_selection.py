@@ -13,7 +13,9 @@ import torch
 from abacus.moe.router import Router
 from oracle import moe_oracle as oracle
 
-SPECIAL_CASES = [(16, 5, torch.float32), (80, 10, torch.bfloat16), (256, 16, torch.float32), (64, 8, torch.bfloat16)]
+SPECIAL_CASES = [(16, 5, torch.float32), (80, 10, torch.bfloat16), (256, 16, torch.float32), (64, 8, torch.bfloat16),
+                 # the wide router (more than 256 experts or 16 slots): logits pass + top-k pass
+                 (40, 24, torch.bfloat16), (300, 20, torch.float32), (1024, 64, torch.bfloat16)]
 
 
 def check_special_selection(E: int, K: int, dtype: torch.dtype, device: torch.device) -> None:

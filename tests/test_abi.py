@@ -65,6 +65,9 @@ def test_abi_version_and_queries():
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 8, _lib.BF16) == 16 * 4096 * 2 + 8 * 1024 * 16 * 4
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 128, _lib.BF16) == 128 * 4096 * 2
     assert _lib.query("abacus_moe_router_ws_bytes", 1024, 17, _lib.F32) == 32 * 1024 * 4
+    # past 256 experts the transposed weight has whole groups of 256 rows (the logits pass)
+    assert _lib.query("abacus_moe_router_ws_bytes", 1024, 300, _lib.BF16) == 512 * 1024 * 2
+    assert _lib.query("abacus_moe_router_ws_bytes", 512, 1024, _lib.F32) == 1024 * 512 * 4
     assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8, _lib.BF16) > 0
     assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8, 7) == -1
     # the down projection's split tail needs a workspace at the Mixtral shape, none for small batches
@@ -76,8 +79,10 @@ def test_abi_version_and_queries():
 @pytest.mark.parametrize(
     "name,args,msg",
     [
-        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 257, 2, 1.0, 1) + (None,) * 8, "n_experts"),
-        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 64, 17, 1.0, 1) + (None,) * 8, "top_k"),
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 1025, 2, 1.0, 1) + (None,) * 8, "n_experts"),
+        ("abacus_moe_router_fwd", (None, None, None, 16, 64, 1024, 65, 1.0, 1) + (None,) * 8, "top_k"),
+        ("abacus_moe_route_scan", (None, 16, 1025, 2, None, 0.0, 1, None, None, None, None), "n_experts"),
+        ("abacus_router_gating_bwd", (None, None, None, 16, 65, 1.0, 1, None, None), "top_k"),
         ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 9, 1.0, 1) + (None,) * 8, "top_k"),
         ("abacus_moe_permute_gather", (None, None, None, 16, 12, 8, 2, 1, None, None, None, None), "dim"),
         ("abacus_moe_router_fwd", (None, None, None, 16, 64, 8, 2, 1.0, 7) + (None,) * 8, "dtype"),

@@ -245,11 +245,18 @@ def test_bf16_odd_shapes(T, D, M, E, K):
     (200, 128, 64, 256, 16, torch.float32),
     (500, 512, 256, 80, 10, torch.bfloat16),
     (257, 64, 96, 65, 1, torch.float32),
-], ids=["E128_K8_bf16", "E256_K16_f32", "E80_K10_bf16", "E65_K1_f32"])
+    (300, 128, 64, 300, 20, torch.bfloat16),
+    (200, 64, 32, 1024, 64, torch.float32),
+    (256, 128, 64, 40, 24, torch.bfloat16),
+    (300, 72, 64, 513, 8, torch.bfloat16),
+], ids=["E128_K8_bf16", "E256_K16_f32", "E80_K10_bf16", "E65_K1_f32", "E300_K20_bf16", "E1024_K64_f32",
+        "E40_K24_bf16", "E513_K8_bf16"])
 def test_wide_expert_counts(T, D, M, E, K, dtype):
-    """Router sizes beyond 64 experts and 8 slots (up to the library's 256 and 16; the reference's
-    Router takes any E >= 1, 1 <= K <= E, router.py:25-28): routing bit-exact against the oracle
-    on the kernel's logits, then the layer against the oracle."""
+    """Router sizes beyond 64 experts and 8 slots, up to the library's 1024 and 64 (past 256
+    experts or 16 slots the router runs as a logits pass and a top-k pass, and the dispatch and
+    backward kernels take their 64-slot forms; the reference's Router takes any E >= 1,
+    1 <= K <= E, router.py:25-28): routing bit-exact against the oracle on the kernel's logits,
+    then the layer against the oracle."""
     print(f"\n[moe-wide] T={T} D={D} M={M} E={E} K={K} {dtype}", flush=True)
     torch.manual_seed(E + K)
     moe = MoE(D, E, K, hidden_dim=M)

@@ -96,11 +96,13 @@ def test_router_known_answer():
     assert torch.all(indices2[..., 0] == 3) and torch.all(indices2[..., 1] == 1)
 
 
+@pytest.mark.parametrize("E,K", [(8, 3), (300, 20), (64, 40)], ids=["E8_K3", "E300_K20", "E64_K40"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_router_backward_matches_oracle(dtype):
-    """Standalone Router: gradients of sum(weights * g) w.r.t. x and w_DE."""
-    torch.manual_seed(11)
-    T, D, E, K = 50, 64, 8, 3
+def test_router_backward_matches_oracle(dtype, E, K):
+    """Standalone Router: gradients of sum(weights * g) w.r.t. x and w_DE (past 256 experts or 16
+    slots: the wide router, the slot-loop gating backward and the 64-slot weight gradient)."""
+    torch.manual_seed(11 + E + K)
+    T, D = 50, 64
     router = Router(D, E, K, route_scale=1.5).to(device=DEV, dtype=dtype)
     x = torch.randn(T, D, device=DEV, dtype=dtype, requires_grad=True)
     g = torch.randn(T, K, device=DEV, dtype=dtype)
@@ -216,7 +218,10 @@ def test_selection_order_special_values(E, K, dtype):
                                            (4096, 256, 8, 2, torch.bfloat16), (3000, 64, 16, 4, torch.float32),
                                            (5000, 64, 16, 2, torch.bfloat16), (33, 72, 256, 16, torch.bfloat16),
                                            (64, 328, 64, 6, torch.bfloat16), (48, 1032, 16, 4, torch.float32),
-                                           (64, 2048, 64, 6, torch.bfloat16)])
+                                           (64, 2048, 64, 6, torch.bfloat16),
+                                           # more than 256 experts or 16 slots: scan and 64-slot gather
+                                           (100, 64, 300, 20, torch.bfloat16), (40, 128, 1024, 64, torch.float32),
+                                           (16, 64, 520, 7, torch.bfloat16), (70, 96, 48, 33, torch.float32)])
 def test_dispatch_matches_scan_then_gather(T, D, E, K, dtype):
     """abacus_moe_dispatch (one launch when the block histograms hold at most 4096 ints: the gather
     blocks scan them) equals abacus_moe_route_scan + abacus_moe_permute_gather bit for bit:
