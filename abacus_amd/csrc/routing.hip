@@ -186,13 +186,20 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
   constexpr int NTH = NW * 64;
   constexpr bool MMA = MODE != kRouteFromPart;
   constexpr bool EPI = MODE == kRouteFull || MODE == kRouteFromPart;  // runs the top-k epilogue
-  static_assert(!(WLDS && MODE == kRouteLogits), "the logits pass reads the transposed copy");
-  __shared__ float red[MMA ? NW : 1][kRouteTB][EP];
+  // red (the waves' partial logits, written after the main loop) and s_w
+  // (each wave's staged weight rows, used in the main loop) share LDS: wave
+  // w's slice of red is exactly its own s_w buffer (16 x EP floats = 32 rows
+  // of EP bf16), and a wave's LDS accesses run in order.
+  constexpr int RED_BYTES = (MMA ? NW : 1) * kRouteTB * EP * 4;
+  constexpr int SW_BYTES = WLDS ? NW * 32 * WROW : 16;
+  static_assert(!WLDS || !MMA || SW_BYTES == RED_BYTES, "one slice per wave");
+  __shared__ __align__(16) char s_redw[RED_BYTES > SW_BYTES ? RED_BYTES : SW_BYTES];
+  auto red = reinterpret_cast<float(*)[kRouteTB][EP]>(s_redw);
+  auto s_w = reinterpret_cast<char(*)[WLDS ? 32 * WROW : 16]>(s_redw);
   __shared__ float s_sc[EPI ? kRouteTB : 1][EPI ? EP : 1];
   __shared__ float s_sel[EPI ? kRouteTB : 1][EPI ? EP : 1];
   __shared__ int s_cnt[EPI ? EP : 1];
   __shared__ float s_bias[EPI ? EP : 1];
-  __shared__ __align__(16) char s_w[WLDS ? NW : 1][WLDS ? 32 * WROW : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -203,7 +210,15 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
   const int kend = MODE == kRoutePart ? min(D, kbeg + DS) : D;
   // the logits pass: this block's group of EP experts
   const int e_base = MODE == kRouteLogits ? (int)blockIdx.y * EP : 0;
-  if constexpr (MODE == kRouteLogits) wt += (int64_t)e_base * D;
+  if constexpr (MODE == kRouteLogits) {
+    if constexpr (WLDS) {
+      w_src += e_base;  // this group's columns of w_DE
+      if (wt_out != nullptr) wt_out += (int64_t)e_base * D;
+    } else {
+      wt += (int64_t)e_base * D;
+    }
+  }
+  const int e_lim = E - e_base;  // columns of w_DE from w_src on
   if constexpr (EPI) {
     for (int i = tid; i < EP; i += NTH) {
       s_cnt[i] = 0;
@@ -230,7 +245,7 @@ __global__ __launch_bounds__(NW * 64) void router_fwd_kernel(
 #pragma unroll
     for (int j = 0; j < NF; ++j) {
       const int c = lane + 64 * j, rr = c / (EP / 8), cc = c % (EP / 8);
-      r[j] = (kbu + rr < kend && cc * 8 < E) ? ld16(w_src + (int64_t)(kbu + rr) * E + cc * 8) : zero16();
+      r[j] = (kbu + rr < kend && cc * 8 < e_lim) ? ld16(w_src + (int64_t)(kbu + rr) * E + cc * 8) : zero16();
     }
   };
   // WLDS: stage a k-block's chunks in this wave's buffer, read the NF
@@ -854,8 +869,9 @@ constexpr int kGatherBatch = 4;
 // Batches of at most this many tokens combine in column chunks (a wave per
 // token and 64-vector chunk, every slot's loads in flight at once).
 constexpr int64_t kCombineSmallT = 1024;
-// Batches of at most this many tokens run the bf16 router (E <= 64) as
-// kRouterSplit slices of D and a second pass over the partial logits.
+// Batches of at most this many tokens run the bf16 router (E <= 256, rows of
+// 16 bytes) as kRouterSplit slices of D and a second pass over the partial
+// logits.  (At T = 4096, E = 8 the slices measured slower: 13.6 -> 14.8 us.)
 constexpr int64_t kRouterSplitT = 1024;
 
 // ---------------------------------------------------------------------------
@@ -1807,7 +1823,7 @@ extern "C" {
 int64_t abacus_moe_hist_len(int64_t T, int64_t E) { return ((T + kRouteTB - 1) / kRouteTB) * E; }
 
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype) {
-  return router_part_offset(D, E, dtype) + (dtype == kBF16 && e_pad(E) <= 64 ? router_part_bytes(E) : 0);
+  return router_part_offset(D, E, dtype) + (dtype == kBF16 && e_pad(E) <= kMaxE ? router_part_bytes(E) : 0);
 }
 
 int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
@@ -1821,13 +1837,24 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   const int EP = e_pad(E);
   const int nb = (int)((T + kRouteTB - 1) / kRouteTB);
   if (wide_routing(E, K)) {
-    // the logits pass over groups of up to 256 experts, then the top-k pass
-    if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
-    else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
-    ABACUS_CHECK_LAUNCH("router weight transpose");
+    // the logits pass over groups of up to 256 experts, then the top-k pass;
+    // with 16-byte rows of w_DE and x (bf16) it stages w_DE in LDS itself and
+    // its first token block writes the transposed copy
+    const bool wl = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && nb > 0;
+    if (!wl) {
+      if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+      else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+      ABACUS_CHECK_LAUNCH("router weight transpose");
+    }
     if (nb == 0) return 0;
     const int group = std::min(EP, 256);
     const dim3 lgrid((unsigned)nb, (unsigned)(EP / group));
+#define ROUTER_LOGITS_W(NF)                                                                                          \
+  hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true, 4, kRouteLogits>), lgrid, dim3(256), 0, s,              \
+                     (const uint16_t*)x_TD, (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws,        \
+                     (const uint16_t*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE,      \
+                     (uint16_t*)nullptr, (int64_t*)nullptr, (int32_t*)nullptr, (float*)nullptr, (int32_t*)nullptr,   \
+                     (float*)nullptr, 0)
 #define ROUTER_LOGITS(TT, NF)                                                                                       \
   hipLaunchKernelGGL((router_fwd_kernel<TT, NF, false, 4, kRouteLogits>), lgrid, dim3(256), 0, s, (const TT*)x_TD, \
                      (const TT*)wt_ws, (const TT*)nullptr, (TT*)nullptr, (const TT*)bias_E, (int)T, (int)D, (int)E,  \
@@ -1842,12 +1869,22 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
     case 8: ROUTER_LOGITS(TT, 8); break;   \
     default: ROUTER_LOGITS(TT, 16); break; \
   }
-    if (dtype == kBF16) {
+    if (wl) {
+      switch (group / 16) {
+        case 1: ROUTER_LOGITS_W(1); break;
+        case 2: ROUTER_LOGITS_W(2); break;
+        case 3: ROUTER_LOGITS_W(3); break;
+        case 4: ROUTER_LOGITS_W(4); break;
+        case 8: ROUTER_LOGITS_W(8); break;
+        default: ROUTER_LOGITS_W(16); break;
+      }
+    } else if (dtype == kBF16) {
       ROUTER_LOGITS_NF(uint16_t)
     } else {
       ROUTER_LOGITS_NF(float)
     }
 #undef ROUTER_LOGITS_NF
+#undef ROUTER_LOGITS_W
 #undef ROUTER_LOGITS
     ABACUS_CHECK_LAUNCH("router logits");
     const int64_t cpl = (E + 63) / 64;  // selection keys per lane
@@ -1873,7 +1910,11 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   }
   // bf16 with whole 16-byte rows of w_DE and x: the router reads w_DE itself
   // and its block 0 writes the transposed copy (for the backward) as it goes.
-  const bool wlds = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && EP <= 64 && nb > 0;
+  // Past 64 experts only small batches take this path, as D-slices (T = 512,
+  // E = 128: 54 -> 29 us; T = 64, E = 256, D = 7168: 140 -> 54 us); a large
+  // batch of 128 or 256 experts is faster on the transposed copy (T = 4096,
+  // E = 256: 142 against 196 us staged).
+  const bool wlds = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && nb > 0 && (EP <= 64 || T <= kRouterSplitT);
   if (!wlds) {
     if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
     else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
@@ -1886,11 +1927,20 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
                      (const uint16_t*)nullptr, (const uint16_t*)w_DE, (uint16_t*)wt_ws, (const uint16_t*)bias_E,      \
                      (int)T, (int)D, (int)E, (int)K, route_scale, (uint16_t*)logits_TE, (uint16_t*)weights_TK,        \
                      indices_TK, idx_TK, score_TK, hist, part, DS)
-#define ROUTER_SWITCH_NF(MODE, GRID)            \
-  switch (EP / 16) {                            \
-    case 1: ROUTER_LAUNCH_W(1, MODE, GRID); break; \
-    case 2: ROUTER_LAUNCH_W(2, MODE, GRID); break; \
-    case 3: ROUTER_LAUNCH_W(3, MODE, GRID); break; \
+#define ROUTER_SWITCH_NF(MODE, GRID)               \
+  switch (EP / 16) {                               \
+    case 1: ROUTER_LAUNCH_W(1, MODE, GRID); break;  \
+    case 2: ROUTER_LAUNCH_W(2, MODE, GRID); break;  \
+    case 3: ROUTER_LAUNCH_W(3, MODE, GRID); break;  \
+    case 4: ROUTER_LAUNCH_W(4, MODE, GRID); break;  \
+    case 8: ROUTER_LAUNCH_W(8, MODE, GRID); break;  \
+    default: ROUTER_LAUNCH_W(16, MODE, GRID); break; \
+  }
+#define ROUTER_SWITCH_NF_FULL(MODE, GRID)          \
+  switch (EP / 16) {                               \
+    case 1: ROUTER_LAUNCH_W(1, MODE, GRID); break;  \
+    case 2: ROUTER_LAUNCH_W(2, MODE, GRID); break;  \
+    case 3: ROUTER_LAUNCH_W(3, MODE, GRID); break;  \
     default: ROUTER_LAUNCH_W(4, MODE, GRID); break; \
   }
     // Small batches: a block per token block streams all of w_DE through one
@@ -1904,9 +1954,10 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
       ROUTER_SWITCH_NF(kRoutePart, dim3(nb, kRouterSplit))
       ABACUS_CHECK_LAUNCH("router_fwd (slices)");
       ROUTER_SWITCH_NF(kRouteFromPart, dim3(nb))
-    } else {
-      ROUTER_SWITCH_NF(kRouteFull, dim3(nb))
+    } else {  // EP <= 64 here
+      ROUTER_SWITCH_NF_FULL(kRouteFull, dim3(nb))
     }
+#undef ROUTER_SWITCH_NF_FULL
 #undef ROUTER_SWITCH_NF
 #undef ROUTER_LAUNCH_W
     ABACUS_CHECK_LAUNCH("router_fwd");

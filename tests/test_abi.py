@@ -60,10 +60,11 @@ def test_abi_version_and_queries():
     assert lib.abacus_moe_abi_version() == 5
     assert _lib.query("abacus_moe_hist_len", 4096, 8) == (4096 // 16) * 8
     assert _lib.query("abacus_moe_hist_len", 17, 8) == 2 * 8
-    # bf16 with at most 64 experts: the transposed weight, then fp32 partial logits
+    # bf16 with at most 256 experts: the transposed weight, then fp32 partial logits
     # (8 slices of D x 1024 tokens x padded experts) for the split small-batch router
     assert _lib.query("abacus_moe_router_ws_bytes", 4096, 8, _lib.BF16) == 16 * 4096 * 2 + 8 * 1024 * 16 * 4
-    assert _lib.query("abacus_moe_router_ws_bytes", 4096, 128, _lib.BF16) == 128 * 4096 * 2
+    assert _lib.query("abacus_moe_router_ws_bytes", 4096, 128, _lib.BF16) == 128 * 4096 * 2 + 8 * 1024 * 128 * 4
+    assert _lib.query("abacus_moe_router_ws_bytes", 4096, 128, _lib.F32) == 128 * 4096 * 4
     assert _lib.query("abacus_moe_router_ws_bytes", 1024, 17, _lib.F32) == 32 * 1024 * 4
     # past 256 experts the transposed weight has whole groups of 256 rows (the logits pass)
     assert _lib.query("abacus_moe_router_ws_bytes", 1024, 300, _lib.BF16) == 512 * 1024 * 2

@@ -123,11 +123,12 @@ def test_router_backward_matches_oracle(dtype, E, K):
 
 
 @pytest.mark.parametrize("T,D,E,K", [(1, 64, 8, 2), (16, 4096, 32, 2), (700, 2048, 48, 4), (1024, 264, 64, 6),
-                                     (1025, 264, 64, 6)])
+                                     (1025, 264, 64, 6), (300, 520, 128, 8), (64, 1032, 256, 8), (33, 2048, 160, 6),
+                                     (1024, 1024, 256, 16)])
 def test_router_small_batch_slices(T, D, E, K):
-    """bf16 routers with at most 64 experts and at most 1024 tokens sum the logits over 8 slices of D
+    """bf16 routers with at most 256 experts and at most 1024 tokens sum the logits over 8 slices of D
     in a second launch (at D = 264 the last three slices are empty; 1025 tokens take the one-launch
-    path).  Through the C ABI: the transposed weight the slice blocks write into the workspace is
+    path; 160 experts pad to 256).  Through the C ABI: the transposed weight the slice blocks write into the workspace is
     exactly w_DE^T (zero rows past E) and the block histograms count the picks.  Through the module:
     routing bit-exact against the oracle given the kernel's logits, logits close to an fp32
     product, input and weight gradients close to fp64 (xavier-initialised weights, logits O(1))."""
@@ -143,6 +144,7 @@ def test_router_small_batch_slices(T, D, E, K):
 
     dt, st = dtype_code(torch.bfloat16), stream_of(DEV)
     EP = (E + 15) // 16 * 16
+    EP = EP if EP <= 64 else (128 if EP <= 128 else 256)
     logits = torch.empty(T, E, dtype=torch.bfloat16, device=DEV)
     weights = torch.empty(T, K, dtype=torch.bfloat16, device=DEV)
     ind = torch.empty(T, K, dtype=torch.int64, device=DEV)
