@@ -16,9 +16,11 @@
  *     unless named *_i64; score / dlogit buffers are fp32 (fp64 with fp64).
  *   - Return 0 on success, nonzero on a rejected argument (1) or launch
  *     failure (2); abacus_moe_last_error() gives the message (per thread).
- *   - Sizes: T tokens, D model dim, E experts (<= 256), K slots per token
- *     (<= 16), M expert hidden dim, R = T*K routed rows.  D and M must be
- *     multiples of 8 (bf16) or 4 (fp32).
+ *   - Sizes: T tokens, D model dim, E experts (<= 1024), K slots per token
+ *     (<= min(E, 64)), M expert hidden dim, R = T*K routed rows.  D and M must
+ *     be multiples of 8 (bf16) or 4 (fp32).  Up to 256 experts and 16 slots
+ *     the router is one fused kernel; beyond, a logits pass and a top-k pass
+ *     (same results: the routing depends only on the stored logits).
  *   - offsets_E1[e] .. offsets_E1[e+1] are the routed rows of expert e in every
  *     expert-contiguous (R, .) buffer; rows are expert-major and, inside an
  *     expert, in ascending token order (moe.py:72-77).
@@ -58,7 +60,7 @@ int abacus_moe_abi_version(void);
 /* int32 elements of the per-token-block expert histogram (and of `base`). */
 int64_t abacus_moe_hist_len(int64_t T, int64_t E);
 /* bytes of the router workspace used by router_fwd / unpermute_bwd: the
- * transposed router weight and, for bf16 with E <= 64, room for the partial
+ * transposed router weight and, for bf16 with E <= 256, room for the partial
  * logits of router_fwd's split small-batch pass (T <= 1024); independent of T. */
 int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
 /* bytes of the fp32 partial-sum scratch used by router_wgrad for this dtype
@@ -77,7 +79,8 @@ int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E);
  * Outputs: logits_TE (dtype, the exact logits routing used), weights_TK
  * (dtype), indices_TK_i64 (descending selection, ties -> lower expert),
  * idx_TK (int32 copy), score_TK (fp32 value of the dtype-rounded selected
- * sigmoid scores), hist (abacus_moe_hist_len ints). */
+ * sigmoid scores), hist (abacus_moe_hist_len ints).  Every output is
+ * required (past 256 experts or 16 slots the top-k pass reads logits_TE). */
 int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E, int64_t T, int64_t D, int64_t E,
                           int64_t K, double route_scale, int dtype, void* logits_TE, void* weights_TK,
                           int64_t* indices_TK_i64, int32_t* idx_TK, void* score_TK, int32_t* hist, void* wt_ws,
