@@ -141,15 +141,17 @@ def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
         return time.perf_counter() - t0
 
     # Sample size: a step of the reference algorithm costs a fixed part (its per-expert weight
-    # slices and their gradients) plus a part per token, both fitted from 16 and n2 tokens.  The
-    # sample is the most tokens whose predicted step fits a third of the time budget, raised (up to
-    # a 30 s step) until the per-token part is at least three quarters of the step, so the rate
-    # measures the per-token work the GPU is compared on rather than the fixed part.
+    # slices and their gradients, once every expert has tokens) plus a part per token, fitted from
+    # n1 = 256 and n2 = 1024 tokens (16 and T for smaller batches; below a few hundred tokens the
+    # number of active experts still grows, which a fit from 16 tokens reads as per-token cost).
+    # The sample is the most tokens whose predicted step fits a third of the time budget, raised
+    # (up to a 30 s step) until the per-token part is at least three quarters of the step, so the
+    # rate measures the per-token work the GPU is compared on rather than the fixed part.
     run(16)  # warm-up
-    n2 = min(256, wl.tokens)
-    t16, tn2 = run(16), run(n2)
-    per_token = max((tn2 - t16) / max(n2 - 16, 1), 1e-7)
-    fixed = max(t16 - 16 * per_token, 0.0)
+    n1, n2 = (256, min(1024, wl.tokens)) if wl.tokens > 256 else (16, wl.tokens)
+    t1, t2 = run(n1), run(n2)
+    per_token = max((t2 - t1) / max(n2 - n1, 1), 1e-7)
+    fixed = max(t1 - n1 * per_token, 0.0)
     budget_tokens = (target_seconds / 3 - fixed) / per_token
     dominant_tokens = min(3 * fixed / per_token, (30.0 - fixed) / per_token)
     tokens = int(min(wl.tokens, max(16, budget_tokens, dominant_tokens)))
@@ -157,6 +159,11 @@ def cpu_baseline(wl, state, x_cpu, target_cpu, target_seconds):
     while sum(times) < target_seconds and len(times) < 5:
         times.append(run(tokens))
     med = statistics.median(times)
+    if tokens > n2:
+        # refit on the sample's own step: over n1 .. n2 the fixed part can hide most of the
+        # per-token part (the Mixtral shape's 2.8 GB of weights and their gradients)
+        per_token = max((med - t1) / (tokens - n1), 1e-7)
+        fixed = max(t1 - n1 * per_token, 0.0)
     share = tokens * per_token / (fixed + tokens * per_token)
     full_step = fixed + wl.tokens * per_token
     cpu_model = platform.processor() or "unknown"
