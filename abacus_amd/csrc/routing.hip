@@ -155,8 +155,10 @@ __device__ __attribute__((always_inline)) inline int select_top_k(uint64_t (&key
 // Each wave loads its k-blocks' rows of w_DE (32 x E, zero-padded to EP
 // columns) into a private LDS buffer and reads them back transposed
 // (ds_read_b64_tr_b16), so no transposed copy has to be made first; block 0
-// also writes the transposed rows to wt_out, for the backward.  Otherwise the
-// operand is read from wt, the transposed copy.
+// also writes the transposed rows to wt_out, for the backward (the token
+// blocks sharing out those writes, a k-block each, measured slower: Mixtral
+// shape 13.4 -> 16.4 us).  Otherwise the operand is read from wt, the
+// transposed copy.
 //
 // MODE splits the block's work for small batches, where one block streaming
 // all of w_DE is bound by the memory requests one CU keeps in flight:
@@ -502,6 +504,198 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const T* __restrict__ 
   }
   __syncthreads();
   for (int e = tid; e < E; e += 256) hist[(int64_t)blockIdx.x * E + e] = s_cnt[e];
+}
+
+// ---------------------------------------------------------------------------
+// K1c: the bf16 router at large batches for 129 to 256 experts (MODE
+// kRouteFull, with the fused epilogue) and the logits pass beyond 256
+// (kRouteLogits, groups of EP = 256 experts on blockIdx.y).  The fused kernel above
+// streams all of w_DE through every 16-token block, which bounds it by L2 at
+// these expert counts (T = 16384, D = 7168, E = 256: ~0.5 ms for ~3.7 GB of
+// weight reads).  Here a block takes 64 tokens, a wave per 16 of them against
+// all EP experts; the block stages each k-block of w_DE (32 rows x EP,
+// swizzled in 32-byte units, tall_swz) once in LDS, two k-blocks per
+// stage in a double buffer, and the four waves read it transposed
+// (ds_read_b64_tr_b16), so w_DE is streamed once per 64 tokens.  The logits
+// (fp32) then go to LDS, and each wave routes its 16 tokens a token at a time
+// with 64 lanes: the same roundings, selection keys and select_top_k rounds as
+// the fused epilogue (the score is recomputed from the staged logit, the same
+// bits).  The transposed copy of w_DE for the backward is made by the transpose
+// kernel beforehand (written from inside this kernel it cost more than the
+// separate pass).  Needs E and D multiples of 8.
+// ---------------------------------------------------------------------------
+constexpr int kTallTokens = 64;  // tokens per block (4 waves x 16)
+// Batches of at least this many tokens take it, for groups of 256 experts:
+// T = 16384, D = 7168, E = 256: 514 -> 212 us; T = 8192, D = 2048, E = 384
+// (two groups, then the top-k pass): 168 -> 92 us; T = 8192, D = 4096,
+// E = 1024: 555 -> 193 us.  Smaller batches and 128 experts measured slower
+// (T = 4096, E = 256: 208 against 144 us; E = 128: 115 against 56 us).
+constexpr int64_t kTallMinT = 8192;
+
+// Staged k-block rows of w_DE: row k (EP bf16) holds EP / 16 units of 32 bytes,
+// unit j at position j ^ tall_swz(k).  A transposed fragment read takes the
+// same unit of 16 rows (k = 8g + j, g, j < 4, and those rows + 4); the XOR
+// puts the 16 rows in distinct units (eight with 128 experts), so a read
+// spans every bank instead of repeating one 32-byte column.
+template <int UNITS>
+__device__ inline int tall_swz(int k) { return ((k & 3) | ((k >> 1) & 12)) & (UNITS - 1); }
+
+template <int WROW>
+__device__ __attribute__((always_inline)) inline Vec16 read_tr_frag(const char* buf, int f, int lane) {
+  // expert f * 16 + lane % 16, the 8 k at 8 (lane / 16): two transposed reads
+  constexpr int UNITS = WROW / 32;
+  const int grp = lane >> 4, s = lane & 15;
+  const int k = 8 * grp + (s >> 2), in = 8 * (s & 3);
+  typedef short v4i16_t __attribute__((ext_vector_type(4)));
+  const v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)(buf + k * WROW + (f ^ tall_swz<UNITS>(k)) * 32 + in));
+  const v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)(buf + (k + 4) * WROW + (f ^ tall_swz<UNITS>(k + 4)) * 32 + in));
+  Vec16 v;
+  v.w[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+  v.w[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+  v.w[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+  v.w[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+  return v;
+}
+
+template <int NF, int MODE>
+__global__ __launch_bounds__(256) void router_tall_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w_src,
+    const uint16_t* __restrict__ bias, int T_, int D, int E, int K, float route_scale, uint16_t* __restrict__ logits,
+    uint16_t* __restrict__ weights, int64_t* __restrict__ indices, int32_t* __restrict__ idx32,
+    float* __restrict__ score, int32_t* __restrict__ hist) {
+  static_assert(MODE == kRouteFull || MODE == kRouteLogits, "one launch");
+  constexpr bool EPI = MODE == kRouteFull;
+  constexpr int EP = NF * 16;
+  constexpr int KB = 32;                        // k per k-block (one 16x16x32 MFMA step)
+  constexpr int UB = 2;                         // k-blocks per stage
+  constexpr int WROW = EP * 2;                  // bytes per staged row (32-byte units swizzled)
+  constexpr int KB_BYTES = KB * WROW;
+  constexpr int STAGE = UB * KB_BYTES;
+  constexpr int CPR = EP / 8;                   // 16-byte chunks per row
+  constexpr int CPT = UB * KB * CPR / 256;      // chunks per thread per stage
+  static_assert(UB * KB * CPR % 256 == 0, "whole chunks per thread");
+  constexpr int LG_BYTES = 4 * 16 * EP * 4;     // the waves' fp32 logits
+  constexpr int LDS = 2 * STAGE > LG_BYTES ? 2 * STAGE : LG_BYTES;
+  constexpr int CPL = EP / 64;                  // selection keys per lane
+  __shared__ __align__(16) char s_buf[LDS];
+  __shared__ int s_cnt[EPI ? 4 : 1][EPI ? EP : 1];
+  __shared__ float s_bias[EPI ? EP : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int e_base = MODE == kRouteLogits ? (int)blockIdx.y * EP : 0;
+  const int e_lim = E - e_base;  // columns of w_DE from w_src + e_base on
+  w_src += e_base;
+  const int t0 = (int)blockIdx.x * kTallTokens + wave * 16;  // this wave's tokens
+  if constexpr (EPI) {
+    for (int i = tid; i < 4 * EP; i += 256) s_cnt[i / EP][i % EP] = 0;
+    for (int i = tid; i < EP; i += 256) s_bias[i] = i < E ? to_f32<uint16_t>(bias[i]) : 0.f;
+  }
+  const int row = t0 + (lane & 15);
+  const bool row_ok = row < T_;
+  const uint16_t* xrow = x + (int64_t)(row_ok ? row : 0) * D;
+  const int kg = (lane >> 4) * 8;
+  const int nst = (D + UB * KB - 1) / (UB * KB);
+
+  Vec16 wr[CPT], xn[UB];
+  auto load = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = tid + 256 * j, u = c / (KB * CPR), rem = c % (KB * CPR), rr = rem / CPR, cc = rem % CPR;
+      const int k = (st * UB + u) * KB + rr;
+      wr[j] = (k < D && cc * 8 < e_lim) ? ld16(w_src + (int64_t)k * E + cc * 8) : zero16();
+    }
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int k = (st * UB + u) * KB + kg;
+      xn[u] = (row_ok && k < D) ? ld16(xrow + k) : zero16();
+    }
+  };
+  auto store = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      const int c = tid + 256 * j, u = c / (KB * CPR), rem = c % (KB * CPR), rr = rem / CPR, cc = rem % CPR;
+      const int unit = (cc >> 1) ^ tall_swz<EP / 16>(rr);
+      st16(s_buf + b * STAGE + u * KB_BYTES + rr * WROW + unit * 32 + (cc & 1) * 16, wr[j]);
+    }
+  };
+
+  f32x4_t acc[NF];
+#pragma unroll
+  for (int f = 0; f < NF; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int st = 0; st < nst; ++st) {
+    Vec16 xc[UB];
+#pragma unroll
+    for (int u = 0; u < UB; ++u) xc[u] = xn[u];
+    if (st + 1 < nst) load(st + 1);  // in flight during this stage's MFMAs
+    const char* buf = s_buf + (st & 1) * STAGE;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const Vec16 b = read_tr_frag<WROW>(buf + u * KB_BYTES, f, lane);
+        Mma16<uint16_t>::run(acc[f], xc[u], b);
+      }
+    }
+    if (st + 1 < nst) store((st + 1) & 1);  // the other buffer: its reads ended before the last barrier
+    __syncthreads();
+  }
+
+  // acc[f][r]: logit of token t0 + 4 (lane / 16) + r, expert f * 16 + lane % 16
+  float* lg = reinterpret_cast<float*>(s_buf) + wave * 16 * EP;  // this wave's [16][EP]
+#pragma unroll
+  for (int f = 0; f < NF; ++f)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lg[(4 * (lane >> 4) + r) * EP + f * 16 + (lane & 15)] = acc[f][r];
+  // (a wave reads back only its own rows, and its LDS accesses run in order)
+  for (int tok = 0; tok < 16; ++tok) {
+    const int t = t0 + tok;
+    const bool valid = t < T_;
+    if constexpr (!EPI) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int e = lane + 64 * c;
+        if (valid && e < e_lim)
+          logits[(int64_t)t * E + e_base + e] = from_f32<uint16_t>(round_to<uint16_t>(lg[tok * EP + e]));
+      }
+    } else {
+      uint64_t key[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int e = lane + 64 * c;
+        key[c] = 0ull;
+        if (valid && e < E) {
+          const float lr = round_to<uint16_t>(lg[tok * EP + e]);
+          logits[(int64_t)t * E + e] = from_f32<uint16_t>(lr);
+          const float s = round_to<uint16_t>(sigmoid_f32_cr(lr));
+          key[c] = selection_key(round_to<uint16_t>(s + s_bias[e]), e);
+        }
+      }
+      const int my_e = select_top_k<64, CPL>(key, K, lane, valid);
+      const float my_s = round_to<uint16_t>(sigmoid_f32_cr(round_to<uint16_t>(lg[tok * EP + my_e])));
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) sum += __shfl(my_s, k, 64);  // pick order
+      if (valid && lane < K) {
+        atomicAdd(&s_cnt[wave][my_e], 1);
+        const float denom = round_to<uint16_t>(sum);
+        const float w = round_to<uint16_t>(round_to<uint16_t>(my_s / denom) * route_scale);
+        const int64_t o = (int64_t)t * K + lane;
+        weights[o] = from_f32<uint16_t>(w);
+        indices[o] = my_e;
+        idx32[o] = my_e;
+        score[o] = my_s;
+      }
+    }
+  }
+  if constexpr (EPI) {
+    // this wave's 16 tokens are histogram block t0 / 16 (rows exist only for t0 < T)
+    if (t0 < T_)
+      for (int e = lane; e < E; e += 64) hist[(int64_t)(t0 / 16) * E + e] = s_cnt[wave][e];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1841,13 +2035,14 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
     // with 16-byte rows of w_DE and x (bf16) it stages w_DE in LDS itself and
     // its first token block writes the transposed copy
     const bool wl = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && nb > 0;
-    if (!wl) {
+    const int group = std::min(EP, 256);
+    const bool tall = wl && group == 256 && T >= kTallMinT;  // large batches: 64 tokens per block
+    if (!wl || tall) {
       if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
       else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);
       ABACUS_CHECK_LAUNCH("router weight transpose");
     }
     if (nb == 0) return 0;
-    const int group = std::min(EP, 256);
     const dim3 lgrid((unsigned)nb, (unsigned)(EP / group));
 #define ROUTER_LOGITS_W(NF)                                                                                          \
   hipLaunchKernelGGL((router_fwd_kernel<uint16_t, NF, true, 4, kRouteLogits>), lgrid, dim3(256), 0, s,              \
@@ -1869,7 +2064,12 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
     case 8: ROUTER_LOGITS(TT, 8); break;   \
     default: ROUTER_LOGITS(TT, 16); break; \
   }
-    if (wl) {
+    if (tall) {
+      const dim3 tgrid((unsigned)((T + kTallTokens - 1) / kTallTokens), (unsigned)(EP / group));
+      hipLaunchKernelGGL((router_tall_kernel<16, kRouteLogits>), tgrid, dim3(256), 0, s, (const uint16_t*)x_TD,
+                         (const uint16_t*)w_DE, (const uint16_t*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale,
+                         (uint16_t*)logits_TE, nullptr, nullptr, nullptr, nullptr, nullptr);
+    } else if (wl) {
       switch (group / 16) {
         case 1: ROUTER_LOGITS_W(1); break;
         case 2: ROUTER_LOGITS_W(2); break;
@@ -1915,6 +2115,17 @@ int abacus_moe_router_fwd(const void* x_TD, const void* w_DE, const void* bias_E
   // batch of 128 or 256 experts is faster on the transposed copy (T = 4096,
   // E = 256: 142 against 196 us staged).
   const bool wlds = dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && nb > 0 && (EP <= 64 || T <= kRouterSplitT);
+  if (dtype == kBF16 && E % 8 == 0 && D % 8 == 0 && EP == 256 && T >= kTallMinT) {
+    // large batches of 129 to 256 experts: 64 tokens per block share the staged weight rows
+    launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
+    ABACUS_CHECK_LAUNCH("router weight transpose");
+    const dim3 tgrid((unsigned)((T + kTallTokens - 1) / kTallTokens));
+    hipLaunchKernelGGL((router_tall_kernel<16, kRouteFull>), tgrid, dim3(256), 0, s, (const uint16_t*)x_TD,
+                       (const uint16_t*)w_DE, (const uint16_t*)bias_E, (int)T, (int)D, (int)E, (int)K, route_scale,
+                       (uint16_t*)logits_TE, (uint16_t*)weights_TK, indices_TK, idx_TK, score_TK, hist);
+    ABACUS_CHECK_LAUNCH("router_fwd (64-token blocks)");
+    return 0;
+  }
   if (!wlds) {
     if (dtype == kBF16) launch_transpose<uint16_t>(w_DE, wt_ws, (int)D, (int)E, EP, s);
     else launch_transpose<float>(w_DE, wt_ws, (int)D, (int)E, EP, s);

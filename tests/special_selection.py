@@ -16,11 +16,13 @@ from oracle import moe_oracle as oracle
 SPECIAL_CASES = [(16, 5, torch.float32), (80, 10, torch.bfloat16), (256, 16, torch.float32), (64, 8, torch.bfloat16),
                  # the wide router (more than 256 experts or 16 slots): logits pass + top-k pass
                  (40, 24, torch.bfloat16), (300, 20, torch.float32), (1024, 64, torch.bfloat16)]
+# bf16 batches of at least 8192 tokens with 129 or more experts take the router with 64-token blocks
+LARGE_BATCH_CASES = [(256, 8, 8200), (160, 16, 8192), (512, 8, 8250), (1024, 64, 8192)]
 
 
-def check_special_selection(E: int, K: int, dtype: torch.dtype, device: torch.device) -> None:
+def check_special_selection(E: int, K: int, dtype: torch.dtype, device: torch.device, T: int = 200) -> None:
     gen = torch.Generator().manual_seed(E * 31 + K)
-    D, T = 64, 200
+    D = 64
     router = Router(D, E, K, bias_update_speed=0.0, route_scale=1.25)
     choices = torch.tensor([float("nan"), float("inf"), float("-inf"), -0.5, 0.0, 0.25, 0.25, -1.0])
     bias = choices[torch.randint(0, len(choices), (E,), generator=gen)]

@@ -249,8 +249,10 @@ def test_bf16_odd_shapes(T, D, M, E, K):
     (200, 64, 32, 1024, 64, torch.float32),
     (256, 128, 64, 40, 24, torch.bfloat16),
     (300, 72, 64, 513, 8, torch.bfloat16),
+    (8192, 128, 64, 256, 8, torch.bfloat16),
+    (8200, 64, 32, 384, 8, torch.bfloat16),
 ], ids=["E128_K8_bf16", "E256_K16_f32", "E80_K10_bf16", "E65_K1_f32", "E300_K20_bf16", "E1024_K64_f32",
-        "E40_K24_bf16", "E513_K8_bf16"])
+        "E40_K24_bf16", "E513_K8_bf16", "E256_K8_T8192_bf16", "E384_K8_T8200_bf16"])
 def test_wide_expert_counts(T, D, M, E, K, dtype):
     """Router sizes beyond 64 experts and 8 slots, up to the library's 1024 and 64 (past 256
     experts or 16 slots the router runs as a logits pass and a top-k pass, and the dispatch and

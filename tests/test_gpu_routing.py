@@ -13,7 +13,7 @@ from abacus.moe.router import Router
 from bench_inputs import bench_inputs
 from oracle import moe_oracle as oracle
 from routing_check import check_against_torch_topk
-from special_selection import SPECIAL_CASES, check_special_selection
+from special_selection import LARGE_BATCH_CASES, SPECIAL_CASES, check_special_selection
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -124,11 +124,15 @@ def test_router_backward_matches_oracle(dtype, E, K):
 
 @pytest.mark.parametrize("T,D,E,K", [(1, 64, 8, 2), (16, 4096, 32, 2), (700, 2048, 48, 4), (1024, 264, 64, 6),
                                      (1025, 264, 64, 6), (300, 520, 128, 8), (64, 1032, 256, 8), (33, 2048, 160, 6),
-                                     (1024, 1024, 256, 16)])
+                                     (1024, 1024, 256, 16), (8200, 264, 256, 8), (8192, 136, 160, 16),
+                                     (8250, 72, 512, 8), (8210, 128, 264, 4)])
 def test_router_small_batch_slices(T, D, E, K):
     """bf16 routers with at most 256 experts and at most 1024 tokens sum the logits over 8 slices of D
     in a second launch (at D = 264 the last three slices are empty; 1025 tokens take the one-launch
-    path; 160 experts pad to 256).  Through the C ABI: the transposed weight the slice blocks write into the workspace is
+    path; 160 experts pad to 256).  From 8192 tokens with 129 or more experts the router runs
+    64-token blocks sharing staged weight rows (with 512 and 264 experts as the logits pass over
+    groups of 256 before the top-k pass; T = 8200, 8210, 8250 leave partial 64-token and 16-token
+    blocks).  Through the C ABI: the transposed weight the slice blocks write into the workspace is
     exactly w_DE^T (zero rows past E) and the block histograms count the picks.  Through the module:
     routing bit-exact against the oracle given the kernel's logits, logits close to an fp32
     product, input and weight gradients close to fp64 (xavier-initialised weights, logits O(1))."""
@@ -144,7 +148,7 @@ def test_router_small_batch_slices(T, D, E, K):
 
     dt, st = dtype_code(torch.bfloat16), stream_of(DEV)
     EP = (E + 15) // 16 * 16
-    EP = EP if EP <= 64 else (128 if EP <= 128 else 256)
+    EP = EP if EP <= 64 else (128 if EP <= 128 else (EP + 255) // 256 * 256)
     logits = torch.empty(T, E, dtype=torch.bfloat16, device=DEV)
     weights = torch.empty(T, K, dtype=torch.bfloat16, device=DEV)
     ind = torch.empty(T, K, dtype=torch.int64, device=DEV)
@@ -214,6 +218,13 @@ def test_selection_order_special_values(E, K, dtype):
     """NaN, +-inf, exact ties and zero selections: see tests/special_selection.py."""
     print(f"\n[routing-special] E={E} K={K} {dtype}", flush=True)
     check_special_selection(E, K, dtype, DEV)
+
+
+@pytest.mark.parametrize("E,K,T", LARGE_BATCH_CASES, ids=[f"E{e}_K{k}_T{t}" for e, k, t in LARGE_BATCH_CASES])
+def test_selection_order_special_values_large_batch(E, K, T):
+    """The same special selections through the bf16 router's 64-token blocks (T >= 8192)."""
+    print(f"\n[routing-special-large] E={E} K={K} T={T}", flush=True)
+    check_special_selection(E, K, torch.bfloat16, DEV, T=T)
 
 
 @pytest.mark.parametrize("T,D,E,K,dtype", [(1, 64, 4, 2, torch.float32), (200, 128, 64, 6, torch.bfloat16),
