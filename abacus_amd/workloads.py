@@ -71,7 +71,12 @@ SKEW_BF16_T64 = Workload("skewed_bf16_T64", 1, 64, 2048, 64, 6, 1408, torch.bflo
 SKEW_BF16_T512 = Workload("skewed_bf16_T512", 1, 512, 2048, 64, 6, 1408, torch.bfloat16, 3, backward=False, zipf_bias=True)
 SKEW_BF16_T16K = Workload("skewed_bf16_T16384", 8, 2048, 2048, 64, 6, 1408, torch.bfloat16, 3, zipf_bias=True)
 
-ALL = {w.name: w for w in (TINY_F32, MID_F32, MIXTRAL_BF16, SKEW_BF16_T64, SKEW_BF16_T512, SKEW_BF16_T16K)}
+# A fine-grained layer (the Qwen3-30B-A3B MoE shape: d_model 2048, 128 experts, top-8, expert hidden
+# 768), 4 x 2048 tokens: about 512 rows per expert, short expert products; not one of the reference's
+# benchmark configurations, a measured point for many small experts.
+FINE_BF16 = Workload("finegrained_bf16", 4, 2048, 2048, 128, 8, 768, torch.bfloat16, 5)
+
+ALL = {w.name: w for w in (TINY_F32, MID_F32, MIXTRAL_BF16, SKEW_BF16_T64, SKEW_BF16_T512, SKEW_BF16_T16K, FINE_BF16)}
 
 
 def zipf_bias(n_experts: int, scale: float = 0.1, s: float = 1.2, seed: int = 3) -> torch.Tensor:
