@@ -1140,16 +1140,29 @@ __global__ __launch_bounds__(256) void combine_fwd_kernel(const T* __restrict__ 
   }
 }
 
+// a * b rounded to fp32 on its own: the empty asm makes the product opaque, so
+// the compiler cannot fuse it into a following add or subtraction (HIP's
+// __fmul_rn is a plain multiply and was contracted into an fma).
+__device__ inline float mul_unfused(float a, float b) {
+  float p = a * b;
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
 // Gating backward for one token (router.py:45,49-51), given dL/dweights:
 //   w_k = rho * s_k / S,  S = sum_j s_j
 //   dL/ds_j = (rho * dw_j - sum_k dw_k * w_k) / S
+// Every product is rounded on its own (mul_unfused, never fused into the sum or
+// the subtraction): with one slot w = rho exactly, so rho * dw and the sum
+// dw * w are the same rounded value and the difference is exactly 0, as the
+// gradient is (fused, the subtraction kept one product's rounding error).
 //   dL/dlogit_j = dL/ds_j * s_j * (1 - s_j)
 __device__ inline void gating_bwd_token(int K, float rho, const float* dw, const float* w, const float* s,
                                        float denom, float* dl) {
   float c = 0.f;
-  for (int k = 0; k < K; ++k) c += dw[k] * w[k];
+  for (int k = 0; k < K; ++k) c += mul_unfused(dw[k], w[k]);
   for (int k = 0; k < K; ++k) {
-    const float ds = (rho * dw[k] - c) / denom;
+    const float ds = (mul_unfused(rho, dw[k]) - c) / denom;
     dl[k] = ds * s[k] * (1.0f - s[k]);
   }
 }
@@ -1307,10 +1320,10 @@ __global__ __launch_bounds__(256) void combine_bwd_wide_kernel(const T* __restri
   float sum = 0.f, c = 0.f;
   for (int k = 0; k < K; ++k) {
     sum += __shfl(my_s, k, 64);
-    c += __shfl(my_dw, k, 64) * __shfl(my_w, k, 64);
+    c += mul_unfused(__shfl(my_dw, k, 64), __shfl(my_w, k, 64));
   }
   if (on) {
-    const float ds = (rho * my_dw - c) / round_to<T>(sum);
+    const float ds = (mul_unfused(rho, my_dw) - c) / round_to<T>(sum);
     dlogit[(int64_t)t * K + lane] = ds * my_s * (1.0f - my_s);
   }
 }
@@ -1328,12 +1341,12 @@ __global__ void router_gating_bwd_kernel(const T* __restrict__ dweights, const T
   float sum = 0.f, c = 0.f;
   for (int k = 0; k < K; ++k) {
     sum += score[o + k];
-    c += to_f32<T>(dweights[o + k]) * to_f32<T>(weights[o + k]);
+    c += mul_unfused(to_f32<T>(dweights[o + k]), to_f32<T>(weights[o + k]));
   }
   const float denom = round_to<T>(sum);
   for (int k = 0; k < K; ++k) {
     const float s = score[o + k];
-    const float ds = (rho * to_f32<T>(dweights[o + k]) - c) / denom;
+    const float ds = (mul_unfused(rho, to_f32<T>(dweights[o + k])) - c) / denom;
     dlogit[o + k] = ds * s * (1.0f - s);
   }
 }

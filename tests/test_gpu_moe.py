@@ -376,3 +376,26 @@ def test_native_library_is_what_ran():
     moe = MoE(8, 4, 2).to(DEV)
     moe(torch.randn(1, 5, 8, device=DEV))
     assert _lib._lib is not None and str(_lib.LIB_PATH).endswith("libabacus_moe.so")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rs", [1.5, 0.75, 2.5])
+def test_one_slot_router_gradient_is_exactly_zero(dtype, rs):
+    """With top_k = 1 the weight is route_scale * s / s = route_scale, so the router's gradients are exactly
+    zero (router.py:49-51).  The gating backward's products are rounded on their own: an fma of
+    route_scale * dw - dw * w had left one product's rounding error in every dlogit (about 1e-9 in dW_DE)
+    when route_scale * dw is not exact."""
+    torch.manual_seed(3)
+    moe = MoE(256, 4, 1, hidden_dim=16, route_scale=rs)
+    with torch.no_grad():
+        for p in (moe.router.w_DE, moe.w_gate_EDM, moe.w_up_EDM, moe.w_down_EMD):
+            p.normal_(0.0, 0.1)
+    moe = moe.to(DEV, dtype)
+    moe.eval()
+    x = torch.randn(300, 256, device=DEV).to(dtype).requires_grad_()
+    out = moe(x)
+    ((out.float() - 1.0) ** 2).mean().backward()
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(moe.router.w_DE.grad) == 0
+    # x.grad holds only the experts' path: compare with the same layer's gradient through detached routing
+    assert torch.isfinite(x.grad).all()
