@@ -323,6 +323,38 @@ def _init_expert_weights(n_experts: int, dim: int, hidden: int):
     return gate_EDM, up_EDM, down_EMD
 
 
+def _run_router_pre_hooks(router: torch.nn.Module, x_BLD: torch.Tensor) -> None:
+    """Forward pre-hooks registered on moe.router, called as the reference's self.router(x) would
+    (moe.py:64).  The layer routes inside its fused kernels, so a hook may observe the input but not
+    replace it."""
+    for hid, hook in list(router._forward_pre_hooks.items()):
+        if router._forward_pre_hooks_with_kwargs.get(hid, False):
+            res = hook(router, (x_BLD,), {})
+        else:
+            res = hook(router, (x_BLD,))
+        if res is not None:
+            raise NotImplementedError("a forward pre-hook on moe.router may not replace the router's input: "
+                                      "the MoE layer routes inside its fused kernels")
+
+
+def _run_router_hooks(router: torch.nn.Module, x_BLD: torch.Tensor, weights_TK: torch.Tensor,
+                      indices_TK: torch.Tensor, lead) -> None:
+    """Forward hooks registered on moe.router, called with the router's output for this call,
+    (weights_BLK, indices_BLK) (router.py:40-54), after the bias step as in the reference.  The weights
+    are the routing the layer used, without a gradient path of their own (the layer's gradients flow
+    through its fused node); a hook may observe them but not replace them."""
+    k = indices_TK.shape[-1]
+    output = (weights_TK.reshape(*lead, k), indices_TK.reshape(*lead, k))
+    for hid, hook in list(router._forward_hooks.items()):
+        if router._forward_hooks_with_kwargs.get(hid, False):
+            res = hook(router, (x_BLD,), {}, output)
+        else:
+            res = hook(router, (x_BLD,), output)
+        if res is not None:
+            raise NotImplementedError("a forward hook on moe.router may not replace the router's output: "
+                                      "the MoE layer routes inside its fused kernels")
+
+
 class MoE(torch.nn.Module):
     """Top-k mixture of SwiGLU experts (moe.py:22-86) on MI355X kernels."""
 
@@ -362,9 +394,15 @@ class MoE(torch.nn.Module):
         """
         router = self.router
         _check_operands(x_BLD, router.w_DE, router.expert_bias_E, self.w_gate_EDM, self.w_up_EDM, self.w_down_EMD)
+        if router._forward_pre_hooks:
+            _run_router_pre_hooks(router, x_BLD)
         batch_shape = x_BLD.shape[:-1]
         x_TD = x_BLD.reshape(-1, self.dim)
-        if x_TD.shape[0] == 0:
+        if x_TD.shape[0] == 0:  # the reference routes the empty batch too (moe.py:64-70)
+            if router._forward_hooks:
+                empty_w = x_BLD.new_empty(0, self.top_k)
+                empty_i = torch.empty(0, self.top_k, dtype=torch.int64, device=x_BLD.device)
+                _run_router_hooks(router, x_BLD, empty_w, empty_i, batch_shape)
             return x_BLD
         x_TD = _contig(x_TD)
         record: dict = {}
@@ -388,6 +426,8 @@ class MoE(torch.nn.Module):
         if padded:
             out_TD = out_TD[:, :D]
         router.last_routing = record["routing"]
+        if router._forward_hooks:
+            _run_router_hooks(router, x_BLD, record["routing"].weights_TK, record["routing"].indices_TK, batch_shape)
         return out_TD.reshape(*batch_shape, self.dim)  # (B, L, D)
 
 
