@@ -1921,9 +1921,7 @@ void launch_transpose(const void* w, void* wt, int D, int E, int E_pad, hipStrea
                      E_pad);
 }
 
-// Experts of the router kernel instance for E (a multiple of 16: 16, 32, 48,
-// 64, 128 or 256): the rows of the transposed router weights, zero beyond E.
-// Rows of the transposed router weight: E rounded up to the expert count of
+// Rows of the transposed router weight (zero beyond E): E rounded up to the expert count of
 // the router kernel instance (16 .. 64 by 16, 128, 256, then whole groups of
 // 256 for the logits pass).
 inline int e_pad(int64_t E) {
