@@ -2168,10 +2168,23 @@ int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const v
 // THIN rows, so it runs thin tiles (no DMA of padding rows) and no split tail.
 static bool down_fwd_thin(int64_t R, int64_t E) { return R <= (int64_t)pipe::THIN * E; }
 
+// The split tail pays only for long reductions.  It saves at most 2/3 of one
+// tile's time, and each split tile writes and rereads its slices' fp32
+// partials.  The launch also carries the slices' blocks and a reduce pass
+// (~20 us even when the tail is empty).  bf16, 20 launches each: every M from
+// 512 to 1408 ran slower split at every shape tried (T = 8192, D = 2048,
+// E = 128, K = 8, M = 768: 344 against 293 us).  M = 2816 ran faster or equal
+// (D = 1024, E = 16: 129 against 143 us), and so did M = 14336 (955 against
+// 995 us).
+constexpr int64_t kSplitMinReduction = 2560;
+static bool down_fwd_split(int64_t R, int64_t M, int64_t E) {
+  return !down_fwd_thin(R, E) && M >= kSplitMinReduction;
+}
+
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype) {
   if (check_gemm_shape(R, D, M, E, dtype) || R == 0) return 0;
   const GemmArgs g = args_down_fwd(nullptr, nullptr, nullptr, R, M, D, E, nullptr);
-  if (!pipe_ok<kDownFwd>(dtype, g, (int)R) || down_fwd_thin(R, E)) return 0;  // no split tail
+  if (!pipe_ok<kDownFwd>(dtype, g, (int)R) || !down_fwd_split(R, M, E)) return 0;  // no split tail
   return plan_split<kDownFwd>(g, (int)R).ws_bytes();
 }
 
@@ -2185,7 +2198,7 @@ int abacus_moe_down_fwd(const void* h_RM, const void* w_down_EMD, const int32_t*
       return dtype == kBF16
                  ? launch_rows<uint16_t, kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd")
                  : launch_rows<float, kDownFwd, -1>(g, (int)R, nullptr, -1, true, (hipStream_t)stream, "down_fwd");
-    if (ws != nullptr) {
+    if (ws != nullptr && down_fwd_split(R, M, E)) {
       const SplitPlan plan = plan_split<kDownFwd>(g, (int)R);
       if (plan.on() && ws_bytes >= plan.ws_bytes())
         return dtype == kBF16

@@ -67,7 +67,7 @@ int64_t abacus_moe_router_ws_bytes(int64_t D, int64_t E, int dtype);
  * (-1 for an unknown dtype). */
 int64_t abacus_moe_router_wgrad_ws_bytes(int64_t T, int64_t D, int64_t E, int dtype);
 /* bytes of the split-tail workspace of down_fwd (0: that shape runs no split, which
- * includes small batches: R <= 128 * E). */
+ * includes small batches, R <= 128 * E, and short reductions, M < 2560). */
 int64_t abacus_moe_down_fwd_ws_bytes(int64_t R, int64_t M, int64_t D, int64_t E, int dtype);
 /* bytes of the per-block partial sums and counts used by load_balancing_fwd. */
 int64_t abacus_moe_load_balancing_ws_bytes(int64_t T, int64_t E);
@@ -120,7 +120,7 @@ int abacus_moe_gateup_fwd(const void* x_perm_RD, const void* w_gate_EDM, const v
 
 /* Replaces moe.py:80: y = h @ w_down[e] for every expert.  With a workspace of
  * abacus_moe_down_fwd_ws_bytes bytes (bf16, and fp32 batches large enough for
- * the pipelined kernel), the tiles beyond the whole rounds
+ * the pipelined kernel; reductions M >= 2560), the tiles beyond the whole rounds
  * of the GPU's CUs run as slices of the reduction, whose fp32 partials the
  * workspace holds; ws = NULL (or too small) runs every tile whole.  Either way
  * the same products are summed, in a fixed order: repeated calls agree bit

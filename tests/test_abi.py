@@ -71,9 +71,14 @@ def test_abi_version_and_queries():
     assert _lib.query("abacus_moe_router_ws_bytes", 512, 1024, _lib.F32) == 1024 * 512 * 4
     assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8, _lib.BF16) > 0
     assert _lib.query("abacus_moe_router_wgrad_ws_bytes", 4096, 4096, 8, 7) == -1
-    # the down projection's split tail needs a workspace at the Mixtral shape, none for small batches
+    # the down projection's split tail needs a workspace for long reductions (M >= 2560), none for
+    # small batches or short reductions
     assert _lib.query("abacus_moe_down_fwd_ws_bytes", 8192, 14336, 4096, 8, _lib.BF16) > 0
+    assert _lib.query("abacus_moe_down_fwd_ws_bytes", 16384, 2816, 1024, 16, _lib.BF16) > 0
+    assert _lib.query("abacus_moe_down_fwd_ws_bytes", 16384, 2560, 1024, 16, _lib.F32) > 0
     assert _lib.query("abacus_moe_down_fwd_ws_bytes", 384, 1408, 2048, 64, _lib.BF16) == 0
+    assert _lib.query("abacus_moe_down_fwd_ws_bytes", 65536, 768, 2048, 128, _lib.BF16) == 0
+    assert _lib.query("abacus_moe_down_fwd_ws_bytes", 98304, 2559, 2048, 64, _lib.BF16) == 0
     assert _lib.query("abacus_attention_bwd_ws_bytes", 4, 2048, 16) == 4 * 16 * 2048 * 4
 
 

@@ -133,8 +133,9 @@ def test_pair_results_match_fp64_products():
 
 
 def test_down_fwd_split_tail():
-    """Tiles past the GPU's whole rounds run as reduction slices plus a reduce kernel: same product."""
-    counts, D, M = [1100, 950, 1030, 1010, 990, 1060, 1000, 1052], 4096, 512
+    """Tiles past the GPU's whole rounds run as reduction slices plus a reduce kernel: same product.
+    (The split runs for reductions of at least 2560; M = 2560 is the shortest.)"""
+    counts, D, M = [1100, 950, 1030, 1010, 990, 1060, 1000, 1052], 4096, 2560
     o = _operands(counts, D, M, torch.bfloat16, seed=14)
     E, R = o["E"], o["R"]
     h, w_down = o["h"], torch.randn(E, M, D, device="cuda", generator=torch.Generator(device="cuda").manual_seed(3))
@@ -220,10 +221,11 @@ def test_fp32_row_products_at_pipelined_sizes():
     """fp32 row-grouped products with enough rows for the pipelined kernel (at least one round
     of 256 x 256 tiles per CU on a 256-CU GPU): every remainder class of an expert's last
     tile, an empty and a one-row expert, the down projection's forward with its split tail
-    and without it, each expert's rows against the fp64 product (relative error 1e-5)."""
+    (a reduction of at least 2560) and without it, each expert's rows against the fp64 product
+    (relative error 1e-5)."""
     base = [256, 257, 383, 384, 385, 511, 512, 1, 128, 129, 0, 130]
     counts = [c + (1536 if c > 1 else 0) for c in base] + [4000, 3000]
-    D, M = 1024, 1024
+    D, M = 1024, 2560
     o = _operands(counts, D, M, torch.float32, seed=41)
     E, R = o["E"], o["R"]
     assert R >= 256 * 256 // (D // 256)
