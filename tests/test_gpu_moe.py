@@ -140,7 +140,8 @@ def test_matches_cpu_oracle(wl, backward):
 # ---------------- the oracle's torch ops on the GPU, full sizes ----------------
 # On the exact inputs bench.py times (the host recipe), and on a second draw of every workload's
 # distributions made on the GPU.
-FULL_CASES = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K]
+FULL_CASES = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K,
+              W.FINE_BF16]
 
 
 @pytest.mark.parametrize("wl", FULL_CASES, ids=[w.name for w in FULL_CASES])

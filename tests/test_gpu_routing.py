@@ -20,7 +20,8 @@ DEV = torch.device("cuda", 0)
 
 # (workload, the exact inputs bench.py times?)  Otherwise a second draw of the same
 # distributions, made on the GPU.
-WORKLOADS = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K]
+WORKLOADS = [W.TINY_F32, W.MID_F32, W.MIXTRAL_BF16, W.SKEW_BF16_T64, W.SKEW_BF16_T512, W.SKEW_BF16_T16K,
+             W.FINE_BF16]
 CASES = [(w, True) for w in WORKLOADS] + [(w, False) for w in WORKLOADS if w.dim * w.n_experts >= 2**16]
 
 
