@@ -62,6 +62,10 @@ def parse_args():
                    help="instead of the layer step: time hipBLASLt (torch.mm) on the same per-expert products "
                         "as the four grouped-GEMM entry points, with the workload's own routing (a reference "
                         "point for the GEMM kernels; no fused epilogues)")
+    p.add_argument("--gemm-shapes", action="store_true",
+                   help="instead of the layer step: time the four grouped-GEMM entry points with the workload's "
+                        "rows split as its routing splits them, as E equal experts and as one expert (a dense "
+                        "product), beside hipBLASLt on the dense product of the same size")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="after the timed steps, copy 1 GiB device-to-device once (a known-size kernel "
                         "to scale FETCH_SIZE / WRITE_SIZE counters against)")
@@ -343,6 +347,107 @@ def bench_vendor_gemm(args, wl, moe, x):
             "workload": wl.name, "rows_per_expert": counts, "steps": args.steps, "kinds": res}
 
 
+def bench_gemm_shapes(args, wl, moe, x):
+    """The four grouped-GEMM entry points on the workload's R = T*K rows split three ways -- as
+    its routing splits them, as E equal experts, and as one expert (then each kind is a dense
+    product) -- and hipBLASLt (torch.mm) on that dense product: what the per-expert structure
+    (more weight matrices, ragged row counts) costs each kind, against the vendor library on
+    the product without it.  Operands: N(0,1) rows (gradients N(0,1e-4^2)), the module's
+    weights (expert 0's for the dense case)."""
+    from abacus_amd import _lib
+
+    dev = x.device
+    moe.eval()
+    with torch.no_grad():
+        moe(x)
+    counts = [int(c) for c in moe.router.last_routing.counts_E.tolist()]
+    D, M, E, dt = wl.dim, wl.hidden, wl.n_experts, wl.dtype
+    if dt != torch.bfloat16:
+        raise SystemExit("--gemm-shapes times the bf16 kernels")
+    R = sum(counts)
+    code, s = _lib.dtype_code(dt, dev), _lib.stream_of(dev)
+    call, ptr = _lib.call, _lib.ptr
+    g = torch.Generator(device=dev).manual_seed(wl.seed)
+
+    def act(rows, cols, scale=1.0):
+        return (torch.randn(rows, cols, device=dev, generator=g) * scale).to(dt)
+
+    xp, h = act(R, D), act(R, M)
+    dy, dgate, dup = act(R, D, 1e-4), act(R, M, 1e-4), act(R, M, 1e-4)
+    gate, up = act(R, M), act(R, M)
+    out_rm = [torch.empty(R, M, device=dev, dtype=dt) for _ in range(3)]
+    out_rd = torch.empty(R, D, device=dev, dtype=dt)
+    ctr = _lib.tile_ctr(dev)
+    wg_all, wu_all, wd_all = moe.w_gate_EDM.detach(), moe.w_up_EDM.detach(), moe.w_down_EMD.detach()
+
+    def timed(fn):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) * 1000.0 for a, b in ev)
+
+    def ours(rows):
+        ne = len(rows)
+        wg, wu, wd = wg_all[:ne], wu_all[:ne], wd_all[:ne]
+        dwg, dwu, dwd = torch.empty_like(wg), torch.empty_like(wu), torch.empty_like(wd)
+        offs = torch.tensor([0] + list(torch.tensor(rows).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+        ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, ne, code)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        return {
+            "abacus_moe_gateup_fwd": lambda: call("abacus_moe_gateup_fwd", ptr(xp), ptr(wg), ptr(wu), ptr(offs), R,
+                                                  D, M, ne, code, ptr(out_rm[0]), ptr(out_rm[1]), ptr(out_rm[2]), s),
+            "abacus_moe_down_fwd": lambda: call("abacus_moe_down_fwd", ptr(h), ptr(wd), ptr(offs), R, M, D, ne, code,
+                                                ptr(out_rd), ptr(ws), ws_bytes, s),
+            "abacus_moe_down_bwd": lambda: call("abacus_moe_down_bwd", ptr(dy), ptr(wd), ptr(gate), ptr(up), ptr(h),
+                                                ptr(offs), R, M, D, ne, code, ptr(out_rm[0]), ptr(out_rm[1]),
+                                                ptr(dwd), ptr(ctr), s),
+            "abacus_moe_gateup_bwd": lambda: call("abacus_moe_gateup_bwd", ptr(dgate), ptr(dup), ptr(wg), ptr(wu),
+                                                  ptr(xp), ptr(offs), R, D, M, ne, code, ptr(out_rd), ptr(dwg),
+                                                  ptr(dwu), ptr(ctr), s),
+        }
+
+    # hipBLASLt on the dense products: gate and up as one (R, D) x (D, 2M) product, the
+    # backward's two data-gradient halves as one (R, 2M) x (2M, D), its weight gradients as
+    # one (D, R) x (R, 2M)
+    wgu = torch.cat([wg_all[0], wu_all[0]], dim=1)            # (D, 2M)
+    wgu_t = wgu.t().contiguous()                               # (2M, D)
+    wd_t = wd_all[0].t().contiguous()                          # (D, M)
+    dgu = torch.cat([dgate, dup], dim=1)                       # (R, 2M)
+    xp_t, h_t = xp.t().contiguous(), h.t().contiguous()
+    o_r2m = torch.empty(R, 2 * M, device=dev, dtype=dt)
+    o_d2m = torch.empty(D, 2 * M, device=dev, dtype=dt)
+    o_md = torch.empty(M, D, device=dev, dtype=dt)
+    blas = {
+        "abacus_moe_gateup_fwd": lambda: torch.mm(xp, wgu, out=o_r2m),
+        "abacus_moe_down_fwd": lambda: torch.mm(h, wd_all[0], out=out_rd),
+        "abacus_moe_down_bwd": lambda: (torch.mm(dy, wd_t, out=out_rm[0]), torch.mm(h_t, dy, out=o_md)),
+        "abacus_moe_gateup_bwd": lambda: (torch.mm(dgu, wgu_t, out=out_rd), torch.mm(xp_t, dgu, out=o_d2m)),
+    }
+    layouts = {"routing": counts, "equal": [R // E + (1 if e < R % E else 0) for e in range(E)], "one_expert": [R]}
+    res = {}
+    for name in GEMM_FLOPS_KINDS:
+        row = {}
+        for lay, rows in layouts.items():
+            row[f"{lay}_us"] = round(timed(ours(rows)[name]), 1)
+        row["hipblaslt_dense_us"] = round(timed(blas[name]), 1)
+        fl = GEMM_FLOPS[name] * R * D * M
+        for k in list(row):
+            row[k.replace("_us", "_tflops")] = round(fl / row[k] / 1e6, 1)
+        res[name] = row
+    return {"gemm_shapes": "grouped-GEMM entry points on R rows split three ways; hipBLASLt on the dense product",
+            "workload": wl.name, "R": R, "D": D, "M": M, "rows_per_expert": counts, "steps": args.steps,
+            "kinds": res}
+
+
+GEMM_FLOPS_KINDS = ("abacus_moe_gateup_fwd", "abacus_moe_down_fwd", "abacus_moe_down_bwd", "abacus_moe_gateup_bwd")
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -370,6 +475,9 @@ def main():
     # and run in eval mode, where the bias does not move (router.py:53).
     if args.vendor_gemm:
         print(json.dumps(bench_vendor_gemm(args, wl, moe, x)), flush=True)
+        return
+    if args.gemm_shapes:
+        print(json.dumps(bench_gemm_shapes(args, wl, moe, x)), flush=True)
         return
     moe.train(wl.backward)
     bias0 = moe.router.expert_bias_E.detach().clone()
