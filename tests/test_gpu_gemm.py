@@ -394,3 +394,54 @@ def test_wgrad_tile_loop(counts, D, M):
     for i, out in enumerate(outs):
         for a, b, name in zip(first, out, ("dw_down", "dw_gate", "dw_up")):
             assert torch.equal(a, b), f"stream launch {i}: {name} differs"
+
+
+def test_one_expert_dense_products():
+    """All rows on one expert (the MoE layer with E = 1, a dense SwiGLU block; bench.py --gemm-shapes
+    times it): many full row tiles and a remainder, a down projection long enough for its split tail,
+    and weight gradients reducing over every row (one expert's few output tiles, each hundreds of
+    k-tiles long). Every product of the four entry points against fp64."""
+    counts, D, M = [4100], 512, 2816
+    o = _operands(counts, D, M, torch.bfloat16, seed=41)
+    E, R = o["E"], o["R"]
+    dev = torch.device("cuda")
+    s = _lib.stream_of(dev)
+    nan = lambda *shape: torch.full(shape, float("nan"), dtype=torch.bfloat16, device="cuda")
+    G, U, H, Y = nan(R, M), nan(R, M), nan(R, M), nan(R, D)
+    dG, dU, dX = nan(R, M), nan(R, M), nan(R, D)
+    dWd, dWg, dWu = nan(E, M, D), nan(E, D, M), nan(E, D, M)
+    ws_bytes = _lib.query("abacus_moe_down_fwd_ws_bytes", R, M, D, E, 1)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
+    call("abacus_moe_gateup_fwd", ptr(o["xp"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["offsets"]), R, D, M, E, 1,
+         ptr(G), ptr(U), ptr(H), s)
+    call("abacus_moe_down_fwd", ptr(o["h"]), ptr(o["w_down"]), ptr(o["offsets"]), R, M, D, E, 1, ptr(Y), ptr(ws),
+         ws_bytes, s)
+    call("abacus_moe_down_bwd", ptr(o["dy"]), ptr(o["w_down"]), ptr(o["gate"]), ptr(o["up"]), ptr(o["h"]),
+         ptr(o["offsets"]), R, M, D, E, 1, ptr(dG), ptr(dU), ptr(dWd), ptr(_lib.tile_ctr(dev)), s)
+    call("abacus_moe_gateup_bwd", ptr(o["dgate"]), ptr(o["dup"]), ptr(o["w_gate"]), ptr(o["w_up"]), ptr(o["xp"]),
+         ptr(o["offsets"]), R, D, M, E, 1, ptr(dX), ptr(dWg), ptr(dWu), ptr(_lib.tile_ctr(dev)), s)
+    torch.cuda.synchronize()
+    for name, t in (("G", G), ("U", U), ("H", H), ("Y", Y), ("dG", dG), ("dU", dU), ("dX", dX), ("dW_down", dWd),
+                    ("dW_gate", dWg), ("dW_up", dWu)):
+        assert not torch.isnan(t).any(), f"{name}: elements left unwritten"
+    f = lambda t: t.double().cpu()
+
+    def close(got, want, what, tol=1e-2):
+        err = float((f(got) - want).norm() / want.norm())
+        assert err < tol, f"{what}: relative error {err:.3g}"
+
+    x, wg, wu, wd = f(o["xp"]), f(o["w_gate"][0]), f(o["w_up"][0]), f(o["w_down"][0])
+    close(G, x @ wg, "G")
+    close(U, x @ wu, "U")
+    g, u = f(G), f(U)
+    close(H, g * torch.sigmoid(g) * u, "H")
+    close(Y, f(o["h"]) @ wd, "Y")
+    dh = f(o["dy"]) @ wd.T
+    gg, uu = f(o["gate"]), f(o["up"])
+    sg = torch.sigmoid(gg)
+    close(dG, dh * uu * sg * (1 + gg * (1 - sg)), "dG", 2e-2)
+    close(dU, dh * gg * sg, "dU", 2e-2)
+    close(dWd[0], f(o["h"]).T @ f(o["dy"]), "dW_down")
+    close(dX, f(o["dgate"]) @ wg.T + f(o["dup"]) @ wu.T, "dX")
+    close(dWg[0], x.T @ f(o["dgate"]), "dW_gate")
+    close(dWu[0], x.T @ f(o["dup"]), "dW_up")
